@@ -1,0 +1,113 @@
+/*
+ * w4a8_oracle.h — CPU restatement of the reference W4A8 projection arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP path: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product (knivesysl_xe_amd/) never links or calls it.
+ *
+ * Every function cites the reference file:line it restates; paths are relative
+ * to the reference repository root (SRSWTI/knivesysl-xe). Names follow the
+ * reference: a weight has M output rows and K columns, a batch has T tokens,
+ * outputs are y[T][M].
+ *
+ * Arithmetic modes
+ *   reference mode : activation block 32 (one FP32 scale per (token, K32)),
+ *                    weight group 32 or 64, FP16 scale with the signed zero
+ *                    point in its low nibble (ORC_SCALE_FP16_ZP4).
+ *   config mode    : per-token activation scale (block 0), weight group 64 or
+ *                    128, plain FP16 scale, zero point 0 (ORC_SCALE_FP16).
+ * The int32 "unit" partial is taken over min(weight group, activation block);
+ * it is exact in every mode.
+ */
+#ifndef W4A8_ORACLE_H
+#define W4A8_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_SCALE_FP16 = 0, ORC_SCALE_FP16_ZP4 = 1 };
+enum { ORC_VAR_GEMV = 0, ORC_VAR_FANOUT = 1, ORC_VAR_GEMM = 2 };
+
+/* ---- scalar conversions ---------------------------------------------- */
+uint16_t orc_f32_to_f16(float x);
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float x);
+float orc_bf16_to_f32(uint16_t b);
+float orc_e2m3(uint32_t code);
+uint32_t orc_e2m3_code_at(const uint8_t *payload, int Kt, int row, int col);
+/* element-wise array forms of the conversions above */
+void orc_f32_to_f16_n(const float *x, uint16_t *h, size_t n);
+void orc_f16_to_f32_n(const uint16_t *h, float *x, size_t n);
+void orc_f32_to_bf16_n(const float *x, uint16_t *b, size_t n);
+
+/* ---- activation quantizers ------------------------------------------- */
+/* x[T][K] fp32 -> q[T][K] int8, scale[T][K/block] (block 32) or [T] (block 0),
+ * sum[T][K/32] (exact int32 code sums per K32; may be NULL). */
+int orc_quantize_act(const float *x, int T, int K, int block, int8_t *q,
+                     float *scale, int32_t *sum);
+/* out[i] = (g/(1+exp(-g))) * up[i] */
+void orc_silu_mul(const float *gate, const float *up, float *out, int n);
+/* out[i] = in[i] * rsqrt(mean(in^2)+eps) * (1 + bf16(w[i])) */
+void orc_rmsnorm(const float *in, const uint16_t *w_bf16, int H, float eps,
+                 float *out);
+
+/* ---- weight side ------------------------------------------------------ */
+uint16_t orc_fit_int4_asym(const float *wf, int n, int reserve_nibble,
+                           int contract, int *out_z);
+/* E2M3 fragment payload + block scales -> natural int4 codes [M][K] and
+ * packed FP16|zp scales [M][K/group]; mode 0 = K32 groups, 2 = K64. */
+int orc_repack_e2m3(const uint8_t *payload, const float *block_scale_inv,
+                    int scale_cols, int M, int K, int mode, int contract,
+                    int8_t *codes, uint16_t *scales);
+/* natural codes/scales <-> the reference's lane-major K32 DPAS layout */
+int orc_pack_ref_layout(const int8_t *codes, const uint16_t *scales, int M,
+                        int K, int group, uint8_t *ref_codes,
+                        uint16_t *ref_scales);
+int orc_unpack_ref_layout(const uint8_t *ref_codes, const uint16_t *ref_scales,
+                          int M, int K, int group, int8_t *codes,
+                          uint16_t *scales);
+
+/* ---- split plans ------------------------------------------------------ */
+int orc_gemv_splits(int groups);
+int orc_gemm_splits(int rgroups, int tgroups, int ktiles, int forced);
+/* Per-token split count for a packed GEMM; offsets has segments+1 entries
+ * (NULL for a single segment of T tokens). Returns 0 or -2. */
+int orc_segment_splits(const int *offsets, int segments, int T, int M, int K,
+                       int forced, int *split_per_token);
+
+/* ---- projection ------------------------------------------------------- */
+typedef struct {
+    int M, K, group, scale_enc;
+    const int8_t *codes;     /* [M][K], values in [-8, 7] */
+    const uint16_t *scales;  /* [M][K/group] */
+} orc_weight_t;
+
+typedef struct {
+    int T, K, block;         /* block: 32 or 0 (per token) */
+    const int8_t *q;         /* [T][K] */
+    const float *scale;      /* [T][K/32] or [T] */
+    const int32_t *sum;      /* [T][K/32] */
+} orc_act_t;
+
+/* Exact int32 unit partials P[T][M][K/unit]. */
+int orc_partials(const orc_weight_t *w, const orc_act_t *a, int32_t *P);
+
+/* y[T][M] (fp32 or bf16) for rows [row_begin, row_end); other rows untouched.
+ * split_per_token[T] gives each token's split count. residual is [T][M] fp32
+ * or NULL. */
+int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
+                const int *split_per_token, int contract,
+                const float *residual, int out_bf16, void *y, int row_begin,
+                int row_end);
+
+int orc_num_threads(void);
+void orc_set_num_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

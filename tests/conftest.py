@@ -1,0 +1,19 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path)")
+
+
+@pytest.fixture(scope="session")
+def golden():
+    import numpy as np
+    with np.load(os.path.join(ROOT, "tests", "golden", "w4a8_golden.npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}

@@ -1,0 +1,375 @@
+"""Pins the CPU oracle (oracle/w4a8_oracle.cpp) before it is trusted as the
+checker of the HIP path. Every check here is independent of the oracle's own
+code: numpy's IEEE conversions and integer matmuls, exact rational
+arithmetic, hand-derived order cases, closed forms and invariants. Fixtures
+come from tests/golden/make_golden.py."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32 if a.dtype == np.float32 else np.uint16)
+
+
+# ------------------------------------------------------------------ conversions
+def test_f32_to_f16_matches_numpy_rne():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(200000) * 10.0 ** rng.integers(-9, 6, 200000)).astype(np.float32)
+    special = np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, 1e6, -1e6,
+                        1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 2.0 ** -24, 2.0 ** -25,
+                        3 * 2.0 ** -26, 2.0 ** -26, 5.9604645e-08, 6.097555e-05, 6.1035156e-05,
+                        np.inf, -np.inf, 1e-30, -1e-45], np.float32)
+    x = np.concatenate([x, special])
+    got = O.f32_to_f16(x)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert O.f32_to_f16(np.array([np.nan], np.float32))[0] & 0x7C00 == 0x7C00
+
+
+def test_f16_to_f32_all_codes():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+
+
+def test_bf16_is_nearest_even():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-20, 20, 100000)).astype(np.float32)
+    b = O.f32_to_bf16(x).astype(np.int64)
+    for d in (-1, 1):
+        other = O.bf16_to_f32((b + d).astype(np.uint16)).astype(np.float64)
+        mine = O.bf16_to_f32(b.astype(np.uint16)).astype(np.float64)
+        e_mine = np.abs(mine - x)
+        e_other = np.abs(other - x)
+        assert np.all(e_mine <= e_other)
+        tie = e_mine == e_other
+        assert np.all((b[tie] & 1) == 0)
+
+
+def test_e2m3_table_closed_form():
+    # OCP FP6 E2M3: exponent bias 1, subnormal m/8; positive codes 0..31 are
+    # the 32 values {0, 1/8, ..., 7/8, 1, 9/8, ..., 15/8, 2, ..., 3.75, 4, ..., 7.5}
+    pos = [O.lib().orc_e2m3(c) for c in range(32)]
+    want = [m / 8 for m in range(8)] + [1 + m / 8 for m in range(8)] + \
+           [2 * (1 + m / 8) for m in range(8)] + [4 * (1 + m / 8) for m in range(8)]
+    assert pos == want
+    assert [O.lib().orc_e2m3(c | 0x20) for c in range(32)] == [-v for v in want]
+
+
+def test_e2m3_fragment_addressing_is_a_bijection():
+    # one m16k32 tile holds 512 six-bit codes in 384 bytes; every (row, col)
+    # must own a distinct field and all 3072 bits must be covered
+    Kt = 2
+    seen = set()
+    for row in range(16):
+        for col in range(32):
+            # recover (lane, idx) through the library by planting a one-hot
+            payload = np.zeros(32 * Kt * 384, np.uint8)
+            hits = []
+            for byte in range(384):
+                for bit in range(8):
+                    payload[:] = 0
+                    payload[byte] = 1 << bit
+                    if O.lib().orc_e2m3_code_at(payload.ctypes.data, Kt, row, col) != 0:
+                        hits.append(byte * 8 + bit)
+            assert len(hits) == 6 and hits == list(range(hits[0], hits[0] + 6))
+            seen.add(hits[0] // 6)
+    assert seen == set(range(512))
+
+
+# ------------------------------------------------------------------ quantizer
+@pytest.mark.parametrize("mode", ["finite", "exceptional"])
+@pytest.mark.parametrize("block", [32, 0])
+def test_quantizer_matches_golden(golden, mode, block):
+    key = f"quant_{mode}_b{block}"
+    q, s, sm = O.quantize_act(golden[key + "_x"], block)
+    assert np.array_equal(q, golden[key + "_q"])
+    assert np.array_equal(bits(s), bits(golden[key + "_scale"]))
+    assert np.array_equal(sm, golden[key + "_sum"])
+
+
+def test_quantizer_round_half_even(golden):
+    q, s, _ = O.quantize_act(golden["quant_ties_x"], 32)
+    assert s[0, 0] == 1.0
+    assert np.array_equal(q, golden["quant_ties_q"])
+
+
+def test_quantizer_invariants():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((16, 512)) * rng.uniform(1e-3, 1e3, (16, 1))).astype(np.float32)
+    for block in (32, 0):
+        q, s, sm = O.quantize_act(x, block)
+        w = 32 if block == 32 else 512
+        sb = np.repeat(s.reshape(16, -1), w, axis=1)
+        xb = x.reshape(16, -1, w)
+        # the block's absmax element lands on +-127; error within half a step
+        idx = np.abs(xb).argmax(axis=2)
+        qa = np.take_along_axis(q.reshape(16, -1, w), idx[..., None], 2)[..., 0]
+        assert np.all(np.abs(qa) == 127)
+        assert np.all(np.abs(x - q * sb) <= sb * (0.5 + 1e-6))
+        assert np.array_equal(sm, q.reshape(16, -1, 32).astype(np.int32).sum(axis=2))
+
+
+def test_quantizer_divides_rather_than_multiplies_by_reciprocal():
+    # find inputs where rint(x/s) and rint(x*(1/s)) differ in fp32; the
+    # reference divides (kernels_dpas.cpp:205, 1181)
+    rng = np.random.default_rng(4)
+    for _ in range(2000):
+        mx = np.float32(rng.uniform(0.5, 100.0))
+        s = mx / np.float32(127.0)
+        x = (np.arange(-126, 127, dtype=np.float32) + np.float32(0.5)) * s
+        x = np.nextafter(x, np.float32(0), dtype=np.float32)
+        div = np.rint(x / s)
+        mul = np.rint(x * (np.float32(1.0) / s))
+        diff = np.nonzero(div != mul)[0]
+        if diff.size:
+            blk = np.zeros((1, 32), np.float32)
+            blk[0, 0] = mx
+            blk[0, 1] = x[diff[0]]
+            q, sc, _ = O.quantize_act(blk, 32)
+            assert sc[0, 0] == s
+            assert q[0, 1] == div[diff[0]] != mul[diff[0]]
+            return
+    pytest.skip("no distinguishing case found")
+
+
+def test_silu_mul_and_rmsnorm_close_to_float64():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(4096) * 4).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    got = O.silu_mul(g, u)
+    g64 = g.astype(np.float64)
+    want = g64 / (1 + np.exp(-g64)) * u
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30)) < 4e-7
+    x = rng.standard_normal(5120).astype(np.float32)
+    w = O.f32_to_bf16(rng.standard_normal(5120).astype(np.float32) * 0.1)
+    got = O.rmsnorm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-6) * (1 + O.bf16_to_f32(w).astype(np.float64))
+    assert np.max(np.abs(got - want)) < 1e-5 * np.max(np.abs(want))
+
+
+# ------------------------------------------------------------------ weights
+def test_fit_int4_asym_known_answer():
+    # w = 0.25 * [0..15]: lo=0, hi=3.75 -> s=0.25, zi=-8, q=j-8, centered=j;
+    # least squares keeps s=0.25 exactly; z=-8; fp16(0.25)=0x3400
+    sh, z = O.fit_int4_asym(np.arange(16, dtype=np.float32) * 0.25)
+    assert (sh, z) == (0x3400, -8)
+    # all-zero group: s falls back to 1.0, z = -8, and w=0 reconstructs to 0
+    sh, z = O.fit_int4_asym(np.zeros(32, np.float32))
+    assert (sh, z) == (0x3C00, -8)
+
+
+def test_fit_int4_asym_reserves_nibble_and_keeps_zero():
+    rng = np.random.default_rng(6)
+    for _ in range(200):
+        wf = (rng.standard_normal(32) * rng.uniform(0.01, 2)).astype(np.float32)
+        wf[rng.integers(0, 32)] = 0.0
+        sh, z = O.fit_int4_asym(wf)
+        assert sh & 0xF == 0 and -8 <= z <= 7
+        s = O.f16_to_f32(np.array([sh], np.uint16))[0]
+        q = np.clip(np.rint(wf / s + z), -8, 7)
+        assert np.all((q - z)[wf == 0] == 0)
+        # at most one clamped code at each end of a fitted range; all others
+        # within half a step of the weight
+        inside = (q > -8) & (q < 7)
+        assert np.all(np.abs(wf - s * (q - z))[inside] <= s * 0.5 * (1 + 1e-5))
+
+
+def random_payload(rng, M, K):
+    Kt = K // 32
+    payload = rng.integers(0, 256, size=(M // 16) * Kt * 384, dtype=np.uint8)
+    scale_cols = Kt // 4
+    bs = rng.uniform(0.001, 0.05, size=((M + 127) // 128) * scale_cols).astype(np.float32)
+    return payload, bs, scale_cols
+
+
+def decode_payload(payload, bs, scale_cols, M, K):
+    Kt = K // 32
+    L = O.lib()
+    wf = np.empty((M, K), np.float32)
+    for r in range(M):
+        for k in range(K):
+            kt = k // 32
+            sc = kt if scale_cols == Kt else kt >> 2
+            b = bs[(r >> 4 >> 3) * scale_cols + sc]
+            wf[r, k] = np.float32(L.orc_e2m3(L.orc_e2m3_code_at(payload.ctypes.data, Kt, r, k))) * b
+    return wf
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_repack_e2m3_quantizes_against_stored_scale(mode):
+    rng = np.random.default_rng(7 + mode)
+    M, K = 32, 256
+    payload, bs, scale_cols = random_payload(rng, M, K)
+    codes, scales = O.repack_e2m3(payload, bs, scale_cols, M, K, mode)
+    group = 64 if mode == 2 else 32
+    wf = decode_payload(payload, bs, scale_cols, M, K)
+    ws = O.f16_to_f32(scales & 0xFFF0)
+    z = (scales & 0xF).astype(np.int32)
+    z = np.where(z >= 8, z - 16, z)
+    wsk = np.repeat(ws, group, axis=1)
+    zk = np.repeat(z, group, axis=1)
+    assert np.array_equal(codes, np.clip(np.rint(wf / wsk + zk), -8, 7).astype(np.int8))
+    for r in range(M):
+        for g in range(K // group):
+            sh, zz = O.fit_int4_asym(wf[r, g * group:(g + 1) * group])
+            assert scales[r, g] == (sh | (zz & 0xF))
+
+
+def test_ref_layout_roundtrip_and_dpas_contract():
+    rng = np.random.default_rng(8)
+    M, K = 32, 128
+    for group in (32, 64):
+        codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+        scales = rng.integers(0, 65536, (M, K // group)).astype(np.uint16)
+        rc, rs = O.pack_ref_layout(codes, scales, group)
+        c2, s2 = O.unpack_ref_layout(rc, rs, M, K, group)
+        assert np.array_equal(codes, c2) and np.array_equal(scales, s2)
+    # one-hot: the B-operand contract (kernels_dpas.cpp:13-15, lane-major
+    # 331-337): row n of a row-group owns dwords n*4..n*4+3 of its 256-byte
+    # (row-group, K32) tile; k sits in dword (k%32)/8 at nibble k%8.
+    Kt = K // 32
+    for row, k in [(0, 0), (5, 9), (17, 63), (31, 127), (16, 32)]:
+        codes = np.zeros((M, K), np.int8)
+        codes[row, k] = -1          # nibble 0xF
+        rc, _ = O.pack_ref_layout(codes, np.zeros((M, K // 32), np.uint16), 32)
+        dword = ((row // 16) * Kt + k // 32) * 64 + (row % 16) * 4 + (k % 32) // 8
+        words = rc.view(np.uint32)
+        assert np.count_nonzero(words) == 1
+        assert words[dword] == 0xF << (4 * (k % 8))
+
+
+# ------------------------------------------------------------------ split plans
+def test_split_heuristics_known_values():
+    # derived by reading kernels_dpas.cpp:170-173 and 1226-1250 at the
+    # BASELINE shapes (row-groups = rows/16, t-groups = tokens/8, K32 tiles)
+    assert [O.gemv_splits(g) for g in (1, 4, 5, 256, 320, 2176, 4095, 4096, 9999)] == \
+        [16, 16, 8, 8, 8, 8, 8, 1, 1]
+    assert O.gemm_splits(1088, 1, 160) == 2       # cfg1, one gate/up weight at T=8
+    assert O.gemm_splits(2176, 1, 160) == 1       # cfg1 if the two were concatenated
+    assert O.gemm_splits(320, 64, 544) == 1       # cfg2, M=512
+    assert O.gemm_splits(320, 256, 160) == 1      # cfg3
+    assert O.gemm_splits(320, 1, 160) == 8        # one 8-row segment at N=5120
+    assert O.gemm_splits(3, 1, 4) == 4            # capped by the K32 tile count
+    assert O.gemm_splits(1, 1, 160) == 16
+    assert O.gemm_splits(2048, 1, 160) == 1
+    assert O.gemm_splits(320, 1, 160, forced=4) == 4
+    assert O.gemm_splits(320, 1, 2, forced=16) == 2
+    assert O.gemm_splits(320, 1, 160, forced=3) == 8   # invalid override ignored
+
+
+def test_segment_splits():
+    seg = [0, 17, 81, 381, 893, 1917, 3965]          # cfg4 token counts
+    sp = O.segment_splits(3965, 17408, 5120, seg)
+    assert np.all(sp == 1)
+    sp = O.segment_splits(24, 5120, 5120, [0, 8, 24])
+    assert np.all(sp[:8] == 8) and np.all(sp[8:] == 4)
+    for bad in ([1, 8, 24], [0, 8, 8, 24], [0, 8, 23]):
+        with pytest.raises(ValueError):
+            O.segment_splits(24, 5120, 5120, bad)
+
+
+@pytest.mark.parametrize("K,unit,S", [(4096, 128, 8), (5120, 128, 2), (17408, 64, 8),
+                                      (5120, 128, 1), (17408, 64, 1)])
+def test_config_split_boundaries_fall_on_units(K, unit, S):
+    # the reference splits in K32 tiles, [Kt*s/S, Kt*(s+1)/S); at every
+    # BASELINE config the boundary is also a weight-group boundary, so the
+    # unit-based split of the oracle is the same partition
+    Kt, Nu = K // 32, K // unit
+    for s in range(S + 1):
+        assert (Kt * s // S) * 32 == (Nu * s // S) * unit
+
+
+# ------------------------------------------------------------------ projection
+@pytest.mark.parametrize("name", ["ref32", "ref64", "cfg128", "cfg64"])
+def test_partials_match_numpy_matmul(golden, name):
+    g = lambda k: golden[f"part_{name}_{k}"]
+    group, block, zp = g("meta")
+    P = O.partials(g("codes"), g("scales"), int(group), int(zp), g("q"), np.zeros(1, np.float32),
+                   g("asum"), int(block))
+    assert np.array_equal(P, g("P"))
+
+
+@pytest.mark.parametrize("name", ["ref32", "ref64", "cfg128", "cfg64"])
+@pytest.mark.parametrize("variant", [O.VAR_GEMV, O.VAR_FANOUT, O.VAR_GEMM])
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_exact_cases(golden, name, variant, splits):
+    g = lambda k: golden[f"exact_{name}_{k}"]
+    group, block, zp = (int(v) for v in g("meta"))
+    y = O.project(g("codes"), g("scales"), group, zp, g("q"), g("ascale"), g("asum"), block,
+                  variant, splits)
+    assert np.array_equal(bits(y), bits(g("y")))
+
+
+def test_order_cases(golden):
+    g = lambda k: golden[f"order_{k}"]
+    for var, S, want in zip(g("variants"), g("splits"), g("expected")):
+        variant = [O.VAR_GEMV, O.VAR_FANOUT, O.VAR_GEMM][int(var)]
+        y = O.project(g("codes"), g("scales"), 32, O.SCALE_FP16, g("q"), g("ascale"), g("asum"),
+                      0, variant, int(S))
+        assert np.all(y == want), (var, S, y[0, 0], want)
+
+
+@pytest.mark.parametrize("block,group,enc", [(32, 32, 1), (32, 64, 1), (0, 128, 0), (0, 64, 0)])
+def test_all_ones_gives_K(block, group, enc):
+    # xpu/probe/w4a4_gemm_probe.cpp:13-17: every code 1, every scale 1.0 with
+    # zero point 0 -> each output equals K
+    M, K, T = 32, 512, 3
+    codes = np.ones((M, K), np.int8)
+    scales = np.full((M, K // group), 0x3C00, np.uint16)
+    q = np.ones((T, K), np.int8)
+    asum = np.full((T, K // 32), 32, np.int32)
+    ascale = np.ones((T, K // 32) if block == 32 else T, np.float32)
+    for variant in (O.VAR_GEMV, O.VAR_FANOUT, O.VAR_GEMM):
+        for S in (1, 2, 8, 16):
+            y = O.project(codes, scales, group, enc, q, ascale, asum, block, variant, S)
+            assert np.all(y == K)
+
+
+def test_bf16_output_and_residual():
+    rng = np.random.default_rng(9)
+    M, K, T = 64, 256, 2
+    codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    scales = (np.abs(rng.standard_normal((M, K // 128))) * 0.02).astype(np.float16).view(np.uint16)
+    q, s, sm = O.quantize_act(rng.standard_normal((T, K)).astype(np.float32), 0)
+    res = rng.standard_normal((T, M)).astype(np.float32)
+    for variant in (O.VAR_GEMV, O.VAR_GEMM):
+        y = O.project(codes, scales, 128, 0, q, s, sm, 0, variant, 2)
+        yb = O.project(codes, scales, 128, 0, q, s, sm, 0, variant, 2, out_bf16=True)
+        assert np.array_equal(yb, O.f32_to_bf16(y))
+        yr = O.project(codes, scales, 128, 0, q, s, sm, 0, variant, 2, residual=res)
+        assert np.array_equal(bits(yr), bits((y + res).astype(np.float32)))
+
+
+def gemm_check_input(T, K):
+    """qwn_gemm_check's deterministic activations (kernels_dpas.cpp:2280-2286)."""
+    k = np.arange(K, dtype=np.int64)[None, :]
+    t = np.arange(T, dtype=np.int64)[:, None]
+    mag = np.exp2((((k * 7) + t * 3) % 13) - 6.0)
+    sgn = np.where((((k * 2654435761 + t) & 0xFFFFFFFF) >> 31) != 0, -1.0, 1.0)
+    return np.where(k % 97 == 0, 0.0, sgn * mag).astype(np.float32)
+
+
+def test_gemm_agrees_with_gemv_reference_gate():
+    # the reference's own gate: RC8 GEMM vs per-row GEMV, cos >= 0.9999 per
+    # token row (kernels_dpas.cpp:2264-2333), here on asymmetric K32 weights
+    rng = np.random.default_rng(10)
+    M, K, T = 256, 1024, 8
+    codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    mags = (np.abs(rng.standard_normal((M, K // 32))) * 0.02).astype(np.float16).view(np.uint16)
+    scales = ((mags & 0xFFF0) | (rng.integers(-8, 8, mags.shape) & 0xF)).astype(np.uint16)
+    q, s, sm = O.quantize_act(gemm_check_input(T, K), 32)
+    ref = O.project(codes, scales, 32, 1, q, s, sm, 32, O.VAR_GEMV, O.gemv_splits(M // 16))
+    got = O.project(codes, scales, 32, 1, q, s, sm, 32, O.VAR_GEMM,
+                    O.gemm_splits(M // 16, T // 8, K // 32))
+    for t in range(T):
+        a, b = ref[t].astype(np.float64), got[t].astype(np.float64)
+        assert a @ b / np.sqrt((a @ a) * (b @ b)) >= 0.9999
+    assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-3)) < 1e-3
