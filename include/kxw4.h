@@ -1,0 +1,186 @@
+/*
+ * kxw4.h — C ABI of libkxw4.so, the MI355X (gfx950) W4A8 projection library.
+ *
+ * Drop-in boundary for the projection path of knivesysl-xe: every entry point
+ * below replaces one C++-linkage function of the reference's projection
+ * interface (xpu/src/tq_common.hpp:385-461), with the stream and every scratch
+ * buffer made explicit so the library holds no hidden state. Plain pointers
+ * and sizes only; `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream). All device pointers must be 16-byte aligned. Calls enqueue work and
+ * return without synchronizing (as the reference's in-order queue does).
+ *
+ * Names follow the reference: a weight has M output rows and K columns; a
+ * batch has T tokens; outputs are y[T][M] row-major.
+ *
+ * Return codes: 0 on success, negative on rejected arguments. The reference's
+ * numbers keep their meaning: -1 missing/unprepared operand or wrong tier,
+ * -2 bad shape, offsets or split plan (kernels_dpas.cpp:1336-1367, 1633-1636),
+ * -3 activation not prepared and -4 split plan the fused reduction cannot
+ * close (fan-out, 947-967). -5 names a tier this library does not build and
+ * -6 a HIP runtime error.
+ */
+#ifndef KXW4_H
+#define KXW4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KXW4_ABI_VERSION 1
+
+enum {
+    KXW4_OK = 0,
+    KXW4_EARG = -1,
+    KXW4_ESHAPE = -2,
+    KXW4_EPREP = -3,
+    KXW4_ESPLIT = -4,
+    KXW4_ETIER = -5,
+    KXW4_EHIP = -6
+};
+
+/* Scale encodings. FP16_ZP4 is the reference's packing: FP16 scale whose low
+ * four mantissa bits carry a signed zero point (kernels_dpas.cpp:253-255,
+ * decode 630-634). FP16 is a plain FP16 scale with zero point 0. */
+enum { KXW4_SCALE_FP16 = 0, KXW4_SCALE_FP16_ZP4 = 1 };
+
+/* Element types of activations, residuals and outputs. */
+enum { KXW4_F32 = 0, KXW4_BF16 = 1 };
+
+/* One packed W4 projection (the W4 fields of tq_qmma_weight_t,
+ * tq_common.hpp:49-76).
+ *   codes : M*K/2 bytes. Tiles of 16 rows x 128 K = 1024 bytes, tile
+ *           (rg, kb) at byte (rg*(K/128) + kb)*1024. Inside a tile, lane
+ *           l in [0,64) owns bytes [16l, 16l+16): row rg*16 + l%16, and
+ *           dword i (0..3) holds k = kb*128 + 32i + 8(l/16) + b for
+ *           b = 0..3 in the low nibbles of bytes 0..3 and b = 4..7 in the
+ *           high nibbles. Nibbles are two's-complement int4.
+ *   scales: [M/16][K/group][16] uint16 (row within the row-group fastest).
+ * Requires M % 16 == 0, K % 128 == 0, group in {32, 64, 128}. */
+typedef struct kxw4_weight {
+    int32_t M, K, group, scale_enc;
+    const uint8_t *codes;
+    const uint16_t *scales;
+} kxw4_weight_t;
+
+/* Quantized activations.
+ *   q     : [T][K] int8. Inside every 64-element chunk, byte 16g + 8h + b
+ *           holds k = 32h + 8g + b (g in 0..3, h in 0..1, b in 0..7), the
+ *           operand order of the int8 MFMA.
+ *   scale : [T][K/32] (block 32) or [T] (block 0 = one scale per token).
+ *   sum   : [T][K/32] exact int32 code sums (needed by zero-point weights).
+ * Requires K % 128 == 0. */
+typedef struct kxw4_act {
+    int32_t T, K, block;
+    const int8_t *q;
+    const float *scale;
+    const int32_t *sum;
+} kxw4_act_t;
+
+int kxw4_abi_version(void);
+const char *kxw4_error_string(int code);
+
+/* Bytes of packed codes and number of scale entries of one weight. */
+size_t kxw4_code_bytes(int M, int K);
+size_t kxw4_scale_count(int M, int K, int group);
+
+/* Split plans. choose_gemv_splits, kernels_dpas.cpp:170-173. */
+int kxw4_gemv_splits(int groups);
+/* choose_gemm_splits, kernels_dpas.cpp:1226-1250; forced in {1,2,4,8,16}
+ * replaces the TQ_XPU_GEMM_SPLITS override, anything else = heuristic. */
+int kxw4_gemm_splits(int rgroups, int tgroups, int ktiles, int forced);
+
+/* ---- weights (load time) ------------------------------------------------ */
+
+/* Natural int4 codes [M][K] (int8 values in [-8,7]) and scales [M][K/group]
+ * -> packed layout. Replaces the packing half of x_w4_repack_weight_mode
+ * (kernels_dpas.cpp:403-424) for callers that already hold integer codes. */
+int kxw4_pack_weight(const int8_t *codes, const uint16_t *scales, int M, int K,
+                     int group, uint8_t *out_codes, uint16_t *out_scales,
+                     void *stream);
+
+/* Inverse of kxw4_pack_weight (tests and export). */
+int kxw4_unpack_weight(const kxw4_weight_t *w, int8_t *codes, uint16_t *scales,
+                       void *stream);
+
+/* Reference DPAS layout (lane-major K32 tiles and FP16|zp scales
+ * [M/16][K/group][16], kernels_dpas.cpp:294-342) -> packed layout. Scales are
+ * copied bit for bit; group is 32 or 64 (s4_k64). */
+int kxw4_import_ref_weight(const uint8_t *ref_codes, const uint16_t *ref_scales,
+                           int M, int K, int group, uint8_t *out_codes,
+                           uint16_t *out_scales, void *stream);
+
+/* x_w4_repack_weight_mode (kernels_dpas.cpp:266-344, 403-424): dense-E2M3
+ * fragment payload [M/16][K/32][384 B] and FP32 block scales
+ * [ceil(M/128)][scale_cols] -> asymmetric int4 fit per group with the zero
+ * point in the FP16 scale nibble. mode 0 = K32 groups, 2 = K64 groups; mode 1
+ * (K16) returns KXW4_ETIER. Outputs use KXW4_SCALE_FP16_ZP4. */
+int kxw4_repack_e2m3(const uint8_t *payload, const float *block_scale_inv,
+                     int scale_cols, int M, int K, int mode, uint8_t *out_codes,
+                     uint16_t *out_scales, void *stream);
+
+/* ---- activations ---------------------------------------------------------- */
+
+/* x[T][K] (KXW4_F32 or KXW4_BF16) -> q, scale, sum. block 32 restates
+ * x_quantize_act_s8 / x_quantize_act_chunk (kernels_dpas.cpp:188-223,
+ * 1149-1207); block 0 applies the same formula once per token row. */
+int kxw4_quantize_act(const void *x, int x_dtype, int T, int K, int block,
+                      int8_t *q, float *scale, int32_t *sum, void *stream);
+
+/* x_silu_mul_quant (kernels_dpas.cpp:851-855): hidden = silu(gate)*up
+ * written to out[T][K] (may be NULL), then quantized as kxw4_quantize_act. */
+int kxw4_silu_mul_quant(float *out, const float *gate, const float *up, int T,
+                        int K, int block, int8_t *q, float *scale, int32_t *sum,
+                        void *stream);
+
+/* x_rmsnorm_quant (kernels_dpas.cpp:866-929), batched over T rows:
+ * out = in * rsqrt(mean(in^2) + eps) * (1 + bf16 w), written to out[T][H]
+ * (may be NULL), then quantized as kxw4_quantize_act. */
+int kxw4_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T,
+                       int H, float eps, int block, int8_t *q, float *scale,
+                       int32_t *sum, void *stream);
+
+/* ---- projections -------------------------------------------------------- */
+
+/* x_gemv_w4a8_core arithmetic (kernels_dpas.cpp:586-675) with the
+ * x_gemv_w4a8_prepared dispatch (1631-1680): per token row, K split in
+ * `splits` parts (0 = choose_gemv_splits(M/16)), two alternating
+ * accumulators per split, ordered split sum, optional FP32 residual[T][M].
+ * T in [1, 64]. y is [T][M] of y_dtype. */
+int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
+              const float *residual, int splits, void *stream);
+
+/* x_gemv_w4a8_fanout (kernels_dpas.cpp:945-1102): up to 4 weights with one K
+ * and one group/encoding, one launch, serial accumulator, one split count
+ * choose_gemv_splits(total row-groups). T in [1, 64]. */
+int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
+                     const kxw4_act_t *a, int y_dtype, void *stream);
+
+/* x_gemm_w4a8 (kernels_dpas.cpp:1334-1490): serial accumulator, split count
+ * per packed segment from choose_gemm_splits(M/16, ceil(rows/8), K/32),
+ * ordered split sum. offsets[segments+1] is host memory (NULL with
+ * segments 0 for one segment); segments may have any positive length (the
+ * reference requires multiples of 8). Optional FP32 residual[T][M] is added
+ * after the projection. */
+int kxw4_gemm(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
+              const float *residual, const int *offsets, int segments,
+              int forced_splits, void *stream);
+
+/* Up to 4 weights sharing one activation in one launch (gate+up), each with
+ * its own split plan; otherwise as kxw4_gemm. No counterpart in the
+ * reference, which issues one x_gemm_w4a8 per weight (decode.cpp:1861-1862). */
+int kxw4_gemm_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
+                     const kxw4_act_t *a, int y_dtype, const int *offsets,
+                     int segments, int forced_splits, void *stream);
+
+/* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
+ * else group), from the same unpack and MFMA code as the projections. */
+int kxw4_partials(const kxw4_weight_t *w, const kxw4_act_t *a, int32_t *P,
+                  void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KXW4_H */

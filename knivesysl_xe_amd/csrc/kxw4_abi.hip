@@ -1,0 +1,308 @@
+// kxw4_abi.hip — the C ABI of libkxw4.so (declared in include/kxw4.h):
+// argument checks with the reference's return codes, split plans, and
+// dispatch to the kernels.
+#include "../../include/kxw4.h"
+#include "kxw4_internal.hpp"
+
+#include <algorithm>
+
+using namespace kxw4;
+
+namespace {
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool valid_group(int g) { return g == 32 || g == 64 || g == 128; }
+
+// Shape of one packed weight (x_w4_repack_weight_mode, kernels_dpas.cpp:406).
+bool valid_shape(int M, int K, int group) {
+    return M > 0 && K > 0 && M % 16 == 0 && K % 128 == 0 && valid_group(group);
+}
+
+int check_weight(const kxw4_weight_t *w) {
+    if (!w || !w->codes || !w->scales) return KXW4_EARG;
+    if (!valid_shape(w->M, w->K, w->group)) return KXW4_ESHAPE;
+    if (w->scale_enc != KXW4_SCALE_FP16 && w->scale_enc != KXW4_SCALE_FP16_ZP4) return KXW4_ETIER;
+    return KXW4_OK;
+}
+
+int check_act(const kxw4_act_t *a, int K, int scale_enc) {
+    if (!a || !a->q || !a->scale) return KXW4_ESHAPE;
+    if (a->K != K || a->T <= 0 || (a->block != 0 && a->block != 32)) return KXW4_ESHAPE;
+    if (scale_enc == KXW4_SCALE_FP16_ZP4 && !a->sum) return KXW4_EPREP;
+    return KXW4_OK;
+}
+
+bool valid_split(int s) { return s == 1 || s == 2 || s == 4 || s == 8 || s == 16; }
+
+template <class Args>
+void fill_act(Args &args, const kxw4_act_t *a, int group, int scale_enc, int y_dtype) {
+    args.q = a->q;
+    args.ascale = a->scale;
+    args.asum = a->sum;
+    args.T = a->T;
+    args.K = a->K;
+    args.group = group;
+    args.block = a->block;
+    args.scale_enc = scale_enc;
+    args.y_bf16 = y_dtype == KXW4_BF16 ? 1 : 0;
+}
+
+// Per-segment split counts of one weight (kernels_dpas.cpp:1343-1367).
+int segment_plan(int M, int K, int T, const int *offsets, int segments, int forced, int *ends,
+                 int *splits, int *count) {
+    const int rgroups = M / 16, Kt = K / 32;
+    if (!offsets) {
+        if (segments != 0) return KXW4_ESHAPE;
+        *count = 1;
+        ends[0] = T;
+        splits[0] = kxw4_gemm_splits(rgroups, (T + 7) / 8, Kt, forced);
+        return KXW4_OK;
+    }
+    if (segments < 1 || segments > kMaxSegments || offsets[0] != 0 || offsets[segments] != T)
+        return KXW4_ESHAPE;
+    for (int i = 0; i < segments; ++i) {
+        if (offsets[i + 1] <= offsets[i]) return KXW4_ESHAPE;
+        ends[i] = offsets[i + 1];
+        splits[i] = kxw4_gemm_splits(rgroups, (offsets[i + 1] - offsets[i] + 7) / 8, Kt, forced);
+    }
+    *count = segments;
+    return KXW4_OK;
+}
+
+int gemm_common(const kxw4_weight_t *const *ws, void *const *ys, int count, const kxw4_act_t *a,
+                int y_dtype, const float *residual, const int *offsets, int segments, int forced,
+                int32_t *dbg, hipStream_t st) {
+    if (!ws || !ys || count <= 0 || count > kMaxWeights) return KXW4_EARG;
+    for (int i = 0; i < count; ++i) {
+        const int rc = check_weight(ws[i]);
+        if (rc) return rc;
+        if (!ys[i] && !dbg) return KXW4_EARG;
+        if (ws[i]->K != ws[0]->K || ws[i]->group != ws[0]->group ||
+            ws[i]->scale_enc != ws[0]->scale_enc)
+            return KXW4_ESHAPE;
+    }
+    if (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16) return KXW4_ESHAPE;
+    const int rc = check_act(a, ws[0]->K, ws[0]->scale_enc);
+    if (rc) return rc;
+    const int T = a->T, K = a->K;
+    int ends[kMaxSegments], nseg = 0;
+    int splits[kMaxWeights][kMaxSegments];
+    bool uniform = true;
+    for (int i = 0; i < count; ++i) {
+        const int prc = segment_plan(ws[i]->M, K, T, offsets, segments, forced, ends, splits[i], &nseg);
+        if (prc) return prc;
+        for (int s = 1; s < nseg; ++s) uniform &= splits[i][s] == splits[i][0];
+    }
+    if (T <= 64 && uniform && !dbg) {
+        SkinnyArgs args{};
+        args.count = count;
+        for (int i = 0; i < count; ++i)
+            args.w[i] = {ws[i]->codes, ws[i]->scales, ys[i], ws[i]->M, splits[i][0], 0, 0};
+        fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
+        args.residual = residual;
+        args.variant = kVarGemm;
+        return launch_skinny(args, false, st);
+    }
+    GemmArgs args{};
+    args.count = count;
+    for (int i = 0; i < count; ++i) {
+        args.w[i].codes = ws[i]->codes;
+        args.w[i].scales = ws[i]->scales;
+        args.w[i].y = ys[i];
+        args.w[i].M = ws[i]->M;
+        for (int s = 0; s < nseg; ++s) args.w[i].seg_split[s] = splits[i][s];
+    }
+    fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
+    args.residual = residual;
+    args.dbg = dbg;
+    args.seg_count = nseg;
+    for (int s = 0; s < nseg; ++s) args.seg_end[s] = ends[s];
+    return launch_gemm(args, dbg != nullptr, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int kxw4_abi_version(void) { return KXW4_ABI_VERSION; }
+
+const char *kxw4_error_string(int code) {
+    switch (code) {
+    case KXW4_OK: return "ok";
+    case KXW4_EARG: return "missing operand or wrong tier";
+    case KXW4_ESHAPE: return "bad shape, offsets or split plan";
+    case KXW4_EPREP: return "activation not prepared";
+    case KXW4_ESPLIT: return "split plan not closable in one work-group";
+    case KXW4_ETIER: return "tier not built by this library";
+    case KXW4_EHIP: return "HIP runtime error";
+    default: return "unknown error";
+    }
+}
+
+size_t kxw4_code_bytes(int M, int K) { return (size_t)M * (size_t)K / 2; }
+
+size_t kxw4_scale_count(int M, int K, int group) {
+    return valid_group(group) ? (size_t)M * (size_t)(K / group) : 0;
+}
+
+// kernels_dpas.cpp:170-173.
+int kxw4_gemv_splits(int groups) {
+    if (groups <= 4) return 16;
+    return groups >= 4096 ? 1 : 8;
+}
+
+// kernels_dpas.cpp:1226-1250.
+int kxw4_gemm_splits(int rgroups, int tgroups, int ktiles, int forced) {
+    if (!valid_split(forced)) forced = 0;
+    const long tasks = (long)rgroups * tgroups;
+    if (tasks <= 0) return 1;
+    if (forced) {
+        int s = forced;
+        while (s > 1 && s > ktiles) s >>= 1;
+        return s;
+    }
+    const long want = 128L * 16;
+    if (tasks >= want) return 1;
+    for (int s = 2; s <= 16; s <<= 1) {
+        if (s > ktiles) break;
+        if (tasks * s >= want) return s;
+    }
+    int s = 16;
+    while (s > 1 && s > ktiles) s >>= 1;
+    return s;
+}
+
+int kxw4_pack_weight(const int8_t *codes, const uint16_t *scales, int M, int K, int group,
+                     uint8_t *out_codes, uint16_t *out_scales, void *stream) {
+    if (!codes || !scales || !out_codes || !out_scales) return KXW4_EARG;
+    if (!valid_shape(M, K, group)) return KXW4_ESHAPE;
+    return launch_pack(codes, scales, M, K, group, out_codes, out_scales, as_stream(stream));
+}
+
+int kxw4_unpack_weight(const kxw4_weight_t *w, int8_t *codes, uint16_t *scales, void *stream) {
+    const int rc = check_weight(w);
+    if (rc) return rc;
+    if (!codes) return KXW4_EARG;
+    return launch_unpack(w->codes, w->scales, w->M, w->K, w->group, codes, scales,
+                         as_stream(stream));
+}
+
+int kxw4_import_ref_weight(const uint8_t *ref_codes, const uint16_t *ref_scales, int M, int K,
+                           int group, uint8_t *out_codes, uint16_t *out_scales, void *stream) {
+    if (!ref_codes || !ref_scales || !out_codes || !out_scales) return KXW4_EARG;
+    if (!valid_shape(M, K, group) || group == 128) return KXW4_ESHAPE;
+    return launch_import_ref(ref_codes, ref_scales, M, K, group, out_codes, out_scales,
+                             as_stream(stream));
+}
+
+// x_w4_repack_weight_mode's checks (kernels_dpas.cpp:404-406): -1 missing
+// operand, -2 shape, -3 odd K32 tile count for K64.
+int kxw4_repack_e2m3(const uint8_t *payload, const float *block_scale_inv, int scale_cols, int M,
+                     int K, int mode, uint8_t *out_codes, uint16_t *out_scales, void *stream) {
+    if (!payload || !block_scale_inv || !out_codes || !out_scales || scale_cols <= 0)
+        return KXW4_EARG;
+    if (M <= 0 || K <= 0 || M % 16 || K % 128) return KXW4_ESHAPE;
+    if (mode == 2 && ((K / 32) & 1)) return KXW4_EPREP;
+    if (mode == 1) return KXW4_ETIER;
+    if (mode != 0 && mode != 2) return KXW4_ESHAPE;
+    if (scale_cols != K / 32 && scale_cols != K / 128) return KXW4_ESHAPE;
+    return launch_repack_e2m3(payload, block_scale_inv, scale_cols, M, K, mode == 2 ? 64 : 32,
+                              out_codes, out_scales, as_stream(stream));
+}
+
+int kxw4_quantize_act(const void *x, int x_dtype, int T, int K, int block, int8_t *q, float *scale,
+                      int32_t *sum, void *stream) {
+    if (!x || !q || !scale) return KXW4_EARG;
+    if (T <= 0 || K <= 0 || K % 64 || (block != 0 && block != 32)) return KXW4_ESHAPE;
+    if (x_dtype != KXW4_F32 && x_dtype != KXW4_BF16) return KXW4_ESHAPE;
+    return launch_quantize(x, x_dtype, T, K, block, q, scale, sum, as_stream(stream));
+}
+
+int kxw4_silu_mul_quant(float *out, const float *gate, const float *up, int T, int K, int block,
+                        int8_t *q, float *scale, int32_t *sum, void *stream) {
+    if (!gate || !up || !q || !scale) return KXW4_EARG;
+    if (T <= 0 || K <= 0 || K % 64 || (block != 0 && block != 32)) return KXW4_ESHAPE;
+    return launch_silu_mul_quant(out, gate, up, T, K, block, q, scale, sum, as_stream(stream));
+}
+
+int kxw4_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
+                       int block, int8_t *q, float *scale, int32_t *sum, void *stream) {
+    if (!in || !w || !q || !scale) return KXW4_EARG;
+    if (T <= 0 || H <= 0 || H % 64 || (block != 0 && block != 32)) return KXW4_ESHAPE;
+    return launch_rmsnorm_quant(out, in, w, T, H, eps, block, q, scale, sum, as_stream(stream));
+}
+
+int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
+              const float *residual, int splits, void *stream) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    if (!y) return KXW4_EARG;
+    rc = check_act(a, w->K, w->scale_enc);
+    if (rc) return rc;
+    if (a->T > 64 || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    const int S = splits ? splits : kxw4_gemv_splits(w->M / 16);
+    if (!valid_split(S)) return KXW4_ESHAPE;
+    SkinnyArgs args{};
+    args.count = 1;
+    args.w[0] = {w->codes, w->scales, y, w->M, S, 0, 0};
+    fill_act(args, a, w->group, w->scale_enc, y_dtype);
+    args.residual = residual;
+    args.variant = kVarGemv;
+    return launch_skinny(args, false, as_stream(stream));
+}
+
+// kernels_dpas.cpp:947-967: -1 bad set, -2 non-uniform tier/K or missing
+// output, -3 unprepared activation, -4 split count beyond the fused reducer.
+int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
+                     const kxw4_act_t *a, int y_dtype, void *stream) {
+    if (!ws || !ys || count <= 0 || count > kMaxWeights) return KXW4_EARG;
+    int groups = 0;
+    for (int i = 0; i < count; ++i) {
+        const kxw4_weight_t *w = ws[i];
+        if (!w || !w->codes || !w->scales || !ys[i] || w->K != ws[0]->K ||
+            !valid_shape(w->M, w->K, w->group) || w->group != ws[0]->group ||
+            w->scale_enc != ws[0]->scale_enc)
+            return KXW4_ESHAPE;
+        groups += w->M / 16;
+    }
+    if (!a || !a->q || !a->scale || a->K != ws[0]->K) return KXW4_EPREP;
+    const int rc = check_act(a, ws[0]->K, ws[0]->scale_enc);
+    if (rc) return rc == KXW4_ESHAPE ? KXW4_EPREP : rc;
+    if (a->T > 64 || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    const int S = kxw4_gemv_splits(groups);
+    if (S > 16) return KXW4_ESPLIT;
+    SkinnyArgs args{};
+    args.count = count;
+    for (int i = 0; i < count; ++i)
+        args.w[i] = {ws[i]->codes, ws[i]->scales, ys[i], ws[i]->M, S, 0, 0};
+    fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
+    args.variant = kVarFanout;
+    return launch_skinny(args, false, as_stream(stream));
+}
+
+int kxw4_gemm(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
+              const float *residual, const int *offsets, int segments, int forced_splits,
+              void *stream) {
+    const kxw4_weight_t *ws[1] = {w};
+    void *ys[1] = {y};
+    if (!w) return KXW4_EARG;
+    return gemm_common(ws, ys, 1, a, y_dtype, residual, offsets, segments, forced_splits, nullptr,
+                       as_stream(stream));
+}
+
+int kxw4_gemm_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
+                     const kxw4_act_t *a, int y_dtype, const int *offsets, int segments,
+                     int forced_splits, void *stream) {
+    return gemm_common(ws, ys, count, a, y_dtype, nullptr, offsets, segments, forced_splits,
+                       nullptr, as_stream(stream));
+}
+
+int kxw4_partials(const kxw4_weight_t *w, const kxw4_act_t *a, int32_t *P, void *stream) {
+    if (!w || !P) return KXW4_EARG;
+    const kxw4_weight_t *ws[1] = {w};
+    void *ys[1] = {nullptr};
+    return gemm_common(ws, ys, 1, a, KXW4_F32, nullptr, nullptr, 0, 0, P, as_stream(stream));
+}
+
+}  // extern "C"

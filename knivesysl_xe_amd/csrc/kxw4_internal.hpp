@@ -1,0 +1,76 @@
+// kxw4_internal.hpp — launch interfaces between the C ABI and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kxw4 {
+
+enum { kVarGemv = 0, kVarFanout = 1, kVarGemm = 2 };
+constexpr int kMaxWeights = 4;
+constexpr int kMaxSegments = 8;
+
+struct SkinnyWeight {
+    const uint8_t *codes;
+    const uint16_t *scales;
+    void *y;
+    int M;
+    int S;          // split count
+    int wrg;        // waves per row-group (set by the launcher)
+    int wg_begin;   // first work-group of this weight (set by the launcher)
+};
+
+struct SkinnyArgs {
+    SkinnyWeight w[kMaxWeights];
+    int count;
+    const int8_t *q;
+    const float *ascale;
+    const int32_t *asum;
+    const float *residual;
+    int32_t *dbg;
+    int T, K, group, block, scale_enc, y_bf16, variant;
+};
+
+struct GemmWeight {
+    const uint8_t *codes;
+    const uint16_t *scales;
+    void *y;
+    int M;
+    int nt_begin;                     // first 128-row n-tile (set by the launcher)
+    int seg_split[kMaxSegments];      // split count per packed segment
+};
+
+struct GemmArgs {
+    GemmWeight w[kMaxWeights];
+    int count;
+    const int8_t *q;
+    const float *ascale;
+    const int32_t *asum;
+    const float *residual;
+    int32_t *dbg;
+    int T, K, group, block, scale_enc, y_bf16;
+    int seg_count;
+    int seg_end[kMaxSegments];        // exclusive token end of each segment
+    int n_tiles, t_tiles;             // set by the launcher
+};
+
+int launch_pack(const int8_t *codes, const uint16_t *scales, int M, int K, int group,
+                uint8_t *out_codes, uint16_t *out_scales, hipStream_t st);
+int launch_unpack(const uint8_t *codes, const uint16_t *scales, int M, int K, int group,
+                  int8_t *out_codes, uint16_t *out_scales, hipStream_t st);
+int launch_import_ref(const uint8_t *ref_codes, const uint16_t *ref_scales, int M, int K,
+                      int group, uint8_t *out_codes, uint16_t *out_scales, hipStream_t st);
+int launch_repack_e2m3(const uint8_t *payload, const float *bs, int scale_cols, int M, int K,
+                       int group, uint8_t *out_codes, uint16_t *out_scales, hipStream_t st);
+
+int launch_quantize(const void *x, int x_dtype, int T, int K, int block, int8_t *q,
+                    float *scale, int32_t *sum, hipStream_t st);
+int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T, int K,
+                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
+int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
+                         int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
+
+int launch_skinny(SkinnyArgs &a, bool debug, hipStream_t st);
+int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
+
+}  // namespace kxw4

@@ -1,0 +1,164 @@
+// kxw4_quant.hip — activation quantizers (kernels_dpas.cpp:188-223, 846-929,
+// 1149-1207), one work-group per token row.
+//
+// A producer computes the fp32 value of element k (plain load, SiLU(g)*u, or
+// (1+w) RMSNorm); the quantizer turns it into int8 with
+//   s = absmax/127 (1 when the block max is not positive),
+//   q = clamp(rint(v / s), -127, 127)          (IEEE division, NaN -> -127)
+// over blocks of 32 K (reference mode) or the whole row (per-token mode), and
+// writes exact int32 code sums per K32. Codes are stored in the MFMA slot
+// order of each 64-element chunk (act_slot).
+//
+// Block 32: the 32 lanes of a half wave hold one block, so absmax and sums are
+// half-wave shuffles and each element is produced once. Per-token: a first pass
+// reduces the row absmax across the work-group, a second pass quantizes
+// (producers are recomputed, bit-identically).
+#include "kxw4_device.hpp"
+#include "kxw4_internal.hpp"
+
+namespace kxw4 {
+
+enum Producer { kLoadF32 = 0, kLoadBF16 = 1, kSiluMul = 2, kRmsNorm = 3 };
+
+constexpr int kQThreads = 256;
+
+struct QuantArgs {
+    const void *x;          // f32 / bf16 input, or gate (SiLU), or in (norm)
+    const float *up;        // SiLU up operand
+    const uint16_t *w;      // RMSNorm bf16 weight
+    float *out;             // optional fp32 producer output [T][K]
+    int8_t *q;
+    float *scale;
+    int32_t *sum;
+    int T, K;
+    float eps;
+};
+
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ int half_wave_sum(int v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float block_reduce_max(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < kQThreads / 64; ++i) r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float block_reduce_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < kQThreads / 64; ++i) r += red[i];
+    __syncthreads();
+    return r;
+}
+
+template <int P>
+__device__ __forceinline__ float produce(const QuantArgs &a, int t, int k, float rms_inv) {
+    const size_t i = (size_t)t * a.K + k;
+    if constexpr (P == kLoadF32) {
+        return static_cast<const float *>(a.x)[i];
+    } else if constexpr (P == kLoadBF16) {
+        return bf16_to_float(static_cast<const uint16_t *>(a.x)[i]);
+    } else if constexpr (P == kSiluMul) {
+        const float g = static_cast<const float *>(a.x)[i];
+        return (g / (1.0f + expf(-g))) * a.up[i];
+    } else {
+        const float v = static_cast<const float *>(a.x)[i];
+        return v * rms_inv * (1.0f + bf16_to_float(a.w[k]));
+    }
+}
+
+__device__ __forceinline__ int8_t quantize_one(float v, float s) {
+    return (int8_t)(int)clampf(rintf(v / s), -127.0f, 127.0f);
+}
+
+template <int P, bool PER_TOKEN>
+__global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
+    __shared__ float red[kQThreads / 64];
+    const int t = blockIdx.x;
+    const int K = a.K;
+    const int tid = threadIdx.x;
+    float rms_inv = 0.0f;
+    if constexpr (P == kRmsNorm) {
+        const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
+        float ss = 0.0f;
+        for (int k = tid; k < K; k += kQThreads) ss += row[k] * row[k];
+        ss = block_reduce_sum(ss, red);
+        rms_inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    int8_t *qrow = a.q + (size_t)t * K;
+    float s_tok = 1.0f;
+    if constexpr (PER_TOKEN) {
+        float mx = -INFINITY;
+        for (int k = tid; k < K; k += kQThreads) {
+            const float v = produce<P>(a, t, k, rms_inv);
+            if (a.out) a.out[(size_t)t * K + k] = v;
+            mx = fmaxf(mx, fabsf(v));
+        }
+        mx = block_reduce_max(mx, red);
+        s_tok = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+        if (tid == 0) a.scale[t] = s_tok;
+    }
+    // K % 32 == 0 and kQThreads % 32 == 0: each half wave walks whole blocks.
+    for (int k = tid; k < K; k += kQThreads) {
+        const float v = produce<P>(a, t, k, rms_inv);
+        float s = s_tok;
+        if constexpr (!PER_TOKEN) {
+            if (a.out) a.out[(size_t)t * K + k] = v;
+            const float mx = half_wave_max(fabsf(v));
+            s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+            if ((k & 31) == 0) a.scale[(size_t)t * (K / 32) + (k >> 5)] = s;
+        }
+        const int8_t q = quantize_one(v, s);
+        qrow[(k & ~63) + act_slot(k)] = q;
+        const int bsum = half_wave_sum((int)q);
+        if ((k & 31) == 0 && a.sum) a.sum[(size_t)t * (K / 32) + (k >> 5)] = bsum;
+    }
+}
+
+template <int P>
+static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
+    if (block == 32)
+        hipLaunchKernelGGL((quantize_kernel<P, false>), dim3(a.T), dim3(kQThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((quantize_kernel<P, true>), dim3(a.T), dim3(kQThreads), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int launch_quantize(const void *x, int x_dtype, int T, int K, int block, int8_t *q,
+                    float *scale, int32_t *sum, hipStream_t st) {
+    QuantArgs a{x, nullptr, nullptr, nullptr, q, scale, sum, T, K, 0.0f};
+    return x_dtype == 1 ? launch_q<kLoadBF16>(a, block, st) : launch_q<kLoadF32>(a, block, st);
+}
+
+int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T, int K,
+                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st) {
+    QuantArgs a{gate, up, nullptr, out, q, scale, sum, T, K, 0.0f};
+    return launch_q<kSiluMul>(a, block, st);
+}
+
+int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
+                         int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st) {
+    QuantArgs a{in, nullptr, w, out, q, scale, sum, T, H, eps};
+    return launch_q<kRmsNorm>(a, block, st);
+}
+
+}  // namespace kxw4

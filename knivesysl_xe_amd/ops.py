@@ -1,0 +1,267 @@
+"""Torch-tensor front end of the W4A8 projection library.
+
+The functions mirror the reference's projection interface (xpu/src/
+tq_common.hpp:385-461) one for one, with explicit activation buffers instead
+of the reference's library-global scratch:
+
+    reference                         here
+    x_w4_repack_weight_mode           W4Weight.repack_e2m3
+    (load-time integer codes)         W4Weight.from_codes
+    reference DPAS layout import      W4Weight.from_reference_layout
+    x_quantize_act_s8 / _chunk        quantize_act
+    x_silu_mul_quant                  silu_mul_quant
+    x_rmsnorm_quant (+ chunk)         rmsnorm_quant
+    x_gemv_w4a8[_add|_prepared]       gemv
+    x_gemv_w4a8_fanout                gemv_fanout
+    x_gemm_w4a8                       gemm
+    (one launch for gate+up)          gemm_fanout
+
+Torch provides device memory and the current stream only; every kernel is
+the HIP code in libkxw4.so, reached through ctypes. Tensors must live on a
+GPU; nothing here falls back to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F32, SCALE_FP16, SCALE_FP16_ZP4, check, lib
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return C.c_void_p(t.data_ptr())
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise ValueError(f"unsupported dtype {dt}")
+
+
+@dataclass
+class W4Weight:
+    """One packed projection: the W4 fields of tq_qmma_weight_t
+    (tq_common.hpp:62-72) in the gfx950 tile layout."""
+    M: int
+    K: int
+    group: int
+    scale_enc: int
+    codes: torch.Tensor      # uint8 [M*K/2]
+    scales: torch.Tensor     # int16 bits [M/16 * K/group * 16]
+
+    def c(self) -> _lib.Weight:
+        return _lib.Weight(self.M, self.K, self.group, self.scale_enc,
+                           self.codes.data_ptr(), self.scales.data_ptr())
+
+    @classmethod
+    def empty(cls, M: int, K: int, group: int, scale_enc: int, device="cuda") -> "W4Weight":
+        codes = torch.empty(M * K // 2, dtype=torch.uint8, device=device)
+        scales = torch.empty(M * (K // group), dtype=torch.int16, device=device)
+        return cls(M, K, group, scale_enc, codes, scales)
+
+    @classmethod
+    def from_codes(cls, codes: torch.Tensor, scales: torch.Tensor, group: int,
+                   scale_enc: int = SCALE_FP16) -> "W4Weight":
+        """codes: int8 [M][K] in [-8, 7]; scales: int16 (FP16 bits) [M][K/group]."""
+        M, K = codes.shape
+        w = cls.empty(M, K, group, scale_enc, codes.device)
+        check("kxw4_pack_weight", lib().kxw4_pack_weight(
+            _ptr(codes), _ptr(scales), M, K, group, _ptr(w.codes), _ptr(w.scales), _stream()))
+        return w
+
+    @classmethod
+    def from_reference_layout(cls, ref_codes: torch.Tensor, ref_scales: torch.Tensor, M: int,
+                              K: int, group: int) -> "W4Weight":
+        """The reference's d_s4 / d_s4_scale buffers (kernels_dpas.cpp:294-342)."""
+        w = cls.empty(M, K, group, SCALE_FP16_ZP4, ref_codes.device)
+        check("kxw4_import_ref_weight", lib().kxw4_import_ref_weight(
+            _ptr(ref_codes), _ptr(ref_scales), M, K, group, _ptr(w.codes), _ptr(w.scales),
+            _stream()))
+        return w
+
+    @classmethod
+    def repack_e2m3(cls, payload: torch.Tensor, block_scale_inv: torch.Tensor, scale_cols: int,
+                    M: int, K: int, mode: int) -> "W4Weight":
+        group = 64 if mode == 2 else 32
+        w = cls.empty(M, K, group, SCALE_FP16_ZP4, payload.device)
+        check("kxw4_repack_e2m3", lib().kxw4_repack_e2m3(
+            _ptr(payload), _ptr(block_scale_inv), scale_cols, M, K, mode, _ptr(w.codes),
+            _ptr(w.scales), _stream()))
+        return w
+
+    def unpack(self):
+        codes = torch.empty(self.M, self.K, dtype=torch.int8, device=self.codes.device)
+        scales = torch.empty(self.M, self.K // self.group, dtype=torch.int16,
+                             device=self.codes.device)
+        wc = self.c()
+        check("kxw4_unpack_weight", lib().kxw4_unpack_weight(
+            C.byref(wc), _ptr(codes), _ptr(scales), _stream()))
+        return codes, scales
+
+
+@dataclass
+class QuantAct:
+    """Quantized activations: q [T][K] int8 in MFMA slot order, scale
+    [T][K/32] or [T], exact code sums [T][K/32]."""
+    T: int
+    K: int
+    block: int
+    q: torch.Tensor
+    scale: torch.Tensor
+    sum: torch.Tensor
+
+    def c(self) -> _lib.Act:
+        return _lib.Act(self.T, self.K, self.block, self.q.data_ptr(), self.scale.data_ptr(),
+                        self.sum.data_ptr())
+
+    @classmethod
+    def empty(cls, T: int, K: int, block: int, device="cuda") -> "QuantAct":
+        q = torch.empty(T, K, dtype=torch.int8, device=device)
+        scale = torch.empty((T, K // 32) if block == 32 else (T,), dtype=torch.float32,
+                            device=device)
+        s = torch.empty(T, K // 32, dtype=torch.int32, device=device)
+        return cls(T, K, block, q, scale, s)
+
+
+def slot_permutation(K: int) -> torch.Tensor:
+    """perm[k] = storage position of element k (MFMA slot order per 64-chunk)."""
+    k = torch.arange(K)
+    return (k & ~63) + 16 * ((k >> 3) & 3) + 8 * ((k >> 5) & 1) + (k & 7)
+
+
+def act_from_codes(q: torch.Tensor, scale: torch.Tensor, sums: torch.Tensor,
+                   block: int) -> QuantAct:
+    """Wrap already-quantized natural-order codes (e.g. test fixtures)."""
+    T, K = q.shape
+    perm = slot_permutation(K).to(q.device)
+    qs = torch.empty_like(q)
+    qs[:, perm] = q
+    return QuantAct(T, K, block, qs.contiguous(), scale.contiguous(), sums.contiguous())
+
+
+def act_codes_natural(a: QuantAct) -> torch.Tensor:
+    perm = slot_permutation(a.K).to(a.q.device)
+    return a.q[:, perm]
+
+
+def quantize_act(x: torch.Tensor, block: int = 0) -> QuantAct:
+    T, K = x.shape
+    a = QuantAct.empty(T, K, block, x.device)
+    check("kxw4_quantize_act", lib().kxw4_quantize_act(
+        _ptr(x), _dtype_code(x.dtype), T, K, block, _ptr(a.q), _ptr(a.scale), _ptr(a.sum),
+        _stream()))
+    return a
+
+
+def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor, block: int = 32, keep_hidden=True):
+    T, K = gate.shape
+    a = QuantAct.empty(T, K, block, gate.device)
+    hidden = torch.empty(T, K, dtype=torch.float32, device=gate.device) if keep_hidden else None
+    check("kxw4_silu_mul_quant", lib().kxw4_silu_mul_quant(
+        _ptr(hidden), _ptr(gate), _ptr(up), T, K, block, _ptr(a.q), _ptr(a.scale),
+        _ptr(a.sum), _stream()))
+    return hidden, a
+
+
+def rmsnorm_quant(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, block: int = 32,
+                  keep_normed=True):
+    T, H = x.shape
+    a = QuantAct.empty(T, H, block, x.device)
+    out = torch.empty(T, H, dtype=torch.float32, device=x.device) if keep_normed else None
+    check("kxw4_rmsnorm_quant", lib().kxw4_rmsnorm_quant(
+        _ptr(out), _ptr(x), _ptr(w_bf16_bits), T, H, eps, block, _ptr(a.q), _ptr(a.scale),
+        _ptr(a.sum), _stream()))
+    return out, a
+
+
+def _out(T: int, M: int, dtype, device, out=None):
+    if out is not None:
+        return out
+    return torch.empty(T, M, dtype=dtype, device=device)
+
+
+def gemv(w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None, splits: int = 0,
+         out=None) -> torch.Tensor:
+    y = _out(a.T, w.M, dtype, a.q.device, out)
+    wc, ac = w.c(), a.c()
+    check("kxw4_gemv", lib().kxw4_gemv(C.byref(wc), C.byref(ac), _ptr(y), _dtype_code(dtype),
+                                       _ptr(residual), splits, _stream()))
+    return y
+
+
+def _weight_array(ws: Sequence[W4Weight]):
+    cs = [w.c() for w in ws]
+    arr = (C.POINTER(_lib.Weight) * len(ws))(*[C.pointer(c) for c in cs])
+    return cs, arr
+
+
+def gemv_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, outs=None):
+    ys = outs if outs is not None else [_out(a.T, w.M, dtype, a.q.device) for w in ws]
+    keep, warr = _weight_array(ws)
+    yarr = (C.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
+    ac = a.c()
+    check("kxw4_gemv_fanout", lib().kxw4_gemv_fanout(warr, yarr, len(ws), C.byref(ac),
+                                                     _dtype_code(dtype), _stream()))
+    return ys
+
+
+def _offsets(offsets):
+    if offsets is None:
+        return None, 0
+    arr = (C.c_int * len(offsets))(*[int(o) for o in offsets])
+    return arr, len(offsets) - 1
+
+
+def gemm(w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None, offsets=None,
+         forced_splits: int = 0, out=None) -> torch.Tensor:
+    y = _out(a.T, w.M, dtype, a.q.device, out)
+    off, nseg = _offsets(offsets)
+    wc, ac = w.c(), a.c()
+    check("kxw4_gemm", lib().kxw4_gemm(C.byref(wc), C.byref(ac), _ptr(y), _dtype_code(dtype),
+                                       _ptr(residual), off, nseg, forced_splits, _stream()))
+    return y
+
+
+def gemm_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offsets=None,
+                forced_splits: int = 0, outs=None):
+    ys = outs if outs is not None else [_out(a.T, w.M, dtype, a.q.device) for w in ws]
+    keep, warr = _weight_array(ws)
+    yarr = (C.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
+    off, nseg = _offsets(offsets)
+    ac = a.c()
+    check("kxw4_gemm_fanout", lib().kxw4_gemm_fanout(warr, yarr, len(ws), C.byref(ac),
+                                                     _dtype_code(dtype), off, nseg,
+                                                     forced_splits, _stream()))
+    return ys
+
+
+def partials(w: W4Weight, a: QuantAct) -> torch.Tensor:
+    unit = 32 if a.block == 32 else w.group
+    P = torch.empty(a.T, w.M, w.K // unit, dtype=torch.int32, device=a.q.device)
+    wc, ac = w.c(), a.c()
+    check("kxw4_partials", lib().kxw4_partials(C.byref(wc), C.byref(ac), _ptr(P), _stream()))
+    return P
+
+
+def gemv_splits(groups: int) -> int:
+    return lib().kxw4_gemv_splits(groups)
+
+
+def gemm_splits(rgroups: int, tgroups: int, ktiles: int, forced: int = 0) -> int:
+    return lib().kxw4_gemm_splits(rgroups, tgroups, ktiles, forced)
