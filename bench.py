@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A8 projection path on one MI355X.
+
+Headline: decode MLP gate+up, M=8 tokens, K=5120,
+N=2x17408, G=128, BF16 out -> achieved HBM GB/s. A step is one fan-out
+projection launch (both weights) over resident int8 activations, as in the
+reference's own GEMM/GEMV benches (kernels_dpas.cpp:2146-2195, quantization
+outside the timer). The other BASELINE configs are measured the same way and
+reported under "configs".
+
+Timing: `steps` launches are captured into one HIP graph (torch's capture on
+the stream the library launches on) and replayed once between two
+synchronizations, so the timed region is back-to-back kernels; the launches
+rotate over weight copies totalling > 512 MB so the 256 MB Infinity Cache
+cannot serve them. HIP events on that stream bracket the replay; the kernel's
+average duration is that time / steps. The cpu_baseline leg times the CPU
+oracle (a scalar C++ restatement of the reference arithmetic, OpenMP over
+output rows) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, public spec
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, public spec
+MALL_BYTES = 256 << 20
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def setup(cfg, seed=0):
+    import torch
+    from knivesysl_xe_amd import ops, workloads
+    inp = workloads.generate(cfg, seed)
+    ws = []
+    for c, s in zip(inp.codes, inp.scales):
+        ws.append(ops.W4Weight.from_codes(torch.from_numpy(c).cuda(),
+                                          torch.from_numpy(s.view(np.int16)).cuda(), cfg.group))
+    x = torch.from_numpy(inp.x_bf16.view(np.int16)).cuda().view(torch.bfloat16)
+    act = ops.quantize_act(x, 0)
+    torch.cuda.synchronize()
+    return inp, ws, x, act
+
+
+def make_copies(ws, min_bytes=2 * MALL_BYTES + (64 << 20)):
+    per = sum(w.codes.numel() + 2 * w.scales.numel() for w in ws)
+    n = max(2, math.ceil(min_bytes / per))
+    copies = [ws]
+    for _ in range(n - 1):
+        copies.append([type(w)(w.M, w.K, w.group, w.scale_enc, w.codes.clone(), w.scales.clone())
+                       for w in ws])
+    return copies, per * n
+
+
+def launcher(cfg, act, outs):
+    import torch
+    from knivesysl_xe_amd import ops
+    dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
+    if cfg.kind == "gemv":
+        return lambda w: ops.gemv(w[0], act, dt, out=outs[0])
+    return lambda w: ops.gemm_fanout(w, act, dt, offsets=cfg.offsets, outs=outs)
+
+
+def time_graph(run, copies, steps, warmup):
+    """Capture `steps` launches in one graph, replay it between syncs."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(3):
+            run(copies[i % len(copies)])
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    def capture(n, offset):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                run(copies[(offset + i) % len(copies)])
+        return g
+
+    gw = capture(max(warmup, 1), 0)
+    gt = capture(steps, max(warmup, 1))
+    torch.cuda.synchronize()
+    gw.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    gt.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / 1e3, wall
+
+
+def check_against_oracle(cfg, inp, outs, rows=512):
+    """Bit-exact spot check of the benchmarked outputs on a row subset."""
+    import torch
+    from oracle import oracle as O
+    from knivesysl_xe_amd import workloads
+    q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(inp.x_bf16), 0)
+    for c, sc, y in zip(inp.codes, inp.scales, outs):
+        N = c.shape[0]
+        if cfg.kind == "gemv":
+            variant, sp = O.VAR_GEMV, O.gemv_splits(N // 16)
+        else:
+            variant, sp = O.VAR_GEMM, O.segment_splits(cfg.tokens, N, cfg.K, cfg.offsets)
+        r = min(rows, N)
+        ref = O.project(c, sc, cfg.group, 0, q, s, sm, 0, variant, sp, out_bf16=cfg.out_bf16,
+                        rows=(0, r))
+        got = y[:, :r]
+        got = got.view(torch.int16).cpu().numpy().view(np.uint16) if cfg.out_bf16 \
+            else got.cpu().numpy().view(np.uint32)
+        if not np.array_equal(got, ref[:, :r].view(got.dtype)):
+            return False
+    return True
+
+
+def measure(cfg, steps, warmup):
+    import torch
+    inp, ws, x, act = setup(cfg)
+    dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
+    outs = [torch.empty(cfg.tokens, w.M, dtype=dt, device="cuda") for w in ws]
+    run = launcher(cfg, act, outs)
+    copies, rot_bytes = make_copies(ws)
+    secs, wall = time_graph(run, copies, steps, warmup)
+    run(copies[0])
+    torch.cuda.synchronize()
+    exact = check_against_oracle(cfg, inp, outs)
+    # activation quantization, timed on its own for reference
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    from knivesysl_xe_amd import ops
+    ops.quantize_act(x, 0)
+    e0.record()
+    for _ in range(20):
+        ops.quantize_act(x, 0)
+    e1.record()
+    torch.cuda.synchronize()
+    quant_us = e0.elapsed_time(e1) / 20 * 1e3
+    per = secs / steps
+    res = {
+        "kernel_us": per * 1e6,
+        "GBps": cfg.algorithmic_bytes() / per / 1e9,
+        "TOPS": cfg.ops() / per / 1e12,
+        "bytes": cfg.algorithmic_bytes(),
+        "ops": cfg.ops(),
+        "bound": cfg.bound,
+        "bit_exact_vs_oracle_rows0_512": exact,
+        "rotated_weight_bytes": rot_bytes,
+        "quantize_us": quant_us,
+        "wall_s": wall,
+    }
+    res["roofline_frac"] = (res["GBps"] / HBM_PEAK_GBS if cfg.bound == "hbm"
+                            else res["TOPS"] / INT8_PEAK_TOPS)
+    del copies, ws, outs
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(cfg, budget_s=10.0):
+    """The oracle on the host cores over repeated full passes of `cfg`."""
+    from oracle import oracle as O
+    from knivesysl_xe_amd import workloads
+    O.build()
+    inp = workloads.generate(cfg, 0)
+    q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(inp.x_bf16), 0)
+    splits = [O.segment_splits(cfg.tokens, c.shape[0], cfg.K, cfg.offsets) for c in inp.codes]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for c, sc, sp in zip(inp.codes, inp.scales, splits):
+            O.project(c, sc, cfg.group, 0, q, s, sm, 0, O.VAR_GEMM, sp, out_bf16=cfg.out_bf16)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": cfg.algorithmic_bytes() * reps / el / 1e9, "unit": "GB/s",
+            "cores": O.num_threads(), "kind": "port",
+            "sample": f"{reps} full {cfg.name} passes (both weights, all 8 tokens) in {el:.1f} s; "
+                      "scalar C++ oracle, OpenMP over output rows"}
+
+
+def read_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except ValueError:
+                pass
+    try:
+        return int((vals["fetch_kib"] + vals["write_kib"]) * 1024 * vals["calibration"])
+    except KeyError:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="cfg0,cfg2_m1,cfg2_m512,cfg3,cfg4",
+                    help="extra BASELINE configs to report ('' for none)")
+    ap.add_argument("--extra-steps", type=int, default=50)
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the projection shards column- or row-parallel, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from knivesysl_xe_amd import workloads
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    head = workloads.CONFIGS["cfg1"]
+    log(f"headline {head.note}")
+    r = measure(head, args.steps, args.warmup)
+    log(f"cfg1: {r['kernel_us']:.2f} us/launch, {r['GBps']:.1f} GB/s, exact={r['bit_exact_vs_oracle_rows0_512']}")
+    extra = {}
+    for name in [c for c in args.configs.split(",") if c]:
+        cfg = workloads.CONFIGS[name]
+        log(f"{name}: {cfg.note}")
+        extra[name] = measure(cfg, args.extra_steps, 5)
+        e = extra[name]
+        log(f"{name}: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, {e['TOPS']:.1f} TOPS, "
+            f"frac {e['roofline_frac']:.3f}, exact={e['bit_exact_vs_oracle_rows0_512']}")
+    log("cpu baseline (oracle on host cores)")
+    cpu = cpu_baseline(head, args.cpu_budget)
+    per = r["kernel_us"] / 1e6
+    out = {
+        "metric": "W4A8 GEMV HBM GB/s (M=1,8) + prefill GEMM int8 TOPS, % of MI355X roofline",
+        "value": round(r["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic, seeded: int4 uniform [-8,7], FP16 |N(0,1)|*0.02 scales, "
+                "BF16 N(0,1) activations quantized per token",
+        "config": {"workload": "cfg1: decode MLP gate+up fan-out, M=8 tokens, K=5120, "
+                               "N=2x17408, G=128, BF16 out",
+                   "tokens": 8, "K": 5120, "N": 34816, "group": 128, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("cfg1")},
+        "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()},
+        "bit_exact_vs_oracle": r["bit_exact_vs_oracle_rows0_512"],
+        "quantize_us": round(r["quantize_us"], 2),
+        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in extra.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -48,6 +48,29 @@ void fill_act(Args &args, const kxw4_act_t *a, int group, int scale_enc, int y_d
     args.y_bf16 = y_dtype == KXW4_BF16 ? 1 : 0;
 }
 
+// Token counts up to this take the decode kernel (kxw4_decode.hip), larger
+// ones the LDS-tiled GEMM (kxw4_gemm.hip).
+constexpr int kDecodeMaxT = 64;
+
+template <class Args>
+void fill_plan(Args &args, const kxw4_weight_t *const *ws, void *const *ys, int count,
+               const kxw4_act_t *a, int y_dtype, const float *residual, int32_t *dbg,
+               const int *ends, const int (*splits)[kMaxSegments], int nseg) {
+    args.count = count;
+    for (int i = 0; i < count; ++i) {
+        args.w[i].codes = ws[i]->codes;
+        args.w[i].scales = ws[i]->scales;
+        args.w[i].y = ys[i];
+        args.w[i].M = ws[i]->M;
+        for (int s = 0; s < nseg; ++s) args.w[i].seg_split[s] = splits[i][s];
+    }
+    fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
+    args.residual = residual;
+    args.dbg = dbg;
+    args.seg_count = nseg;
+    for (int s = 0; s < nseg; ++s) args.seg_end[s] = ends[s];
+}
+
 // Per-segment split counts of one weight (kernels_dpas.cpp:1343-1367).
 int segment_plan(int M, int K, int T, const int *offsets, int segments, int forced, int *ends,
                  int *splits, int *count) {
@@ -88,37 +111,32 @@ int gemm_common(const kxw4_weight_t *const *ws, void *const *ys, int count, cons
     const int T = a->T, K = a->K;
     int ends[kMaxSegments], nseg = 0;
     int splits[kMaxWeights][kMaxSegments];
-    bool uniform = true;
     for (int i = 0; i < count; ++i) {
         const int prc = segment_plan(ws[i]->M, K, T, offsets, segments, forced, ends, splits[i], &nseg);
         if (prc) return prc;
-        for (int s = 1; s < nseg; ++s) uniform &= splits[i][s] == splits[i][0];
     }
-    if (T <= 64 && uniform && !dbg) {
-        SkinnyArgs args{};
-        args.count = count;
-        for (int i = 0; i < count; ++i)
-            args.w[i] = {ws[i]->codes, ws[i]->scales, ys[i], ws[i]->M, splits[i][0], 0, 0};
-        fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
-        args.residual = residual;
+    if (T <= kDecodeMaxT) {
+        DecodeArgs args{};
+        fill_plan(args, ws, ys, count, a, y_dtype, residual, dbg, ends, splits, nseg);
         args.variant = kVarGemm;
-        return launch_skinny(args, false, st);
+        return launch_decode(args, dbg != nullptr, st);
     }
     GemmArgs args{};
-    args.count = count;
-    for (int i = 0; i < count; ++i) {
-        args.w[i].codes = ws[i]->codes;
-        args.w[i].scales = ws[i]->scales;
-        args.w[i].y = ys[i];
-        args.w[i].M = ws[i]->M;
-        for (int s = 0; s < nseg; ++s) args.w[i].seg_split[s] = splits[i][s];
-    }
-    fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
-    args.residual = residual;
-    args.dbg = dbg;
-    args.seg_count = nseg;
-    for (int s = 0; s < nseg; ++s) args.seg_end[s] = ends[s];
+    fill_plan(args, ws, ys, count, a, y_dtype, residual, dbg, ends, splits, nseg);
     return launch_gemm(args, dbg != nullptr, st);
+}
+
+// One split count for every token (the GEMV and fan-out GEMV plans).
+int decode_uniform(const kxw4_weight_t *const *ws, void *const *ys, int count,
+                   const kxw4_act_t *a, int y_dtype, const float *residual, int S, int variant,
+                   hipStream_t st) {
+    int ends[1] = {a->T};
+    int splits[kMaxWeights][kMaxSegments];
+    for (int i = 0; i < count; ++i) splits[i][0] = S;
+    DecodeArgs args{};
+    fill_plan(args, ws, ys, count, a, y_dtype, residual, nullptr, ends, splits, 1);
+    args.variant = variant;
+    return launch_decode(args, false, st);
 }
 
 }  // namespace
@@ -240,16 +258,12 @@ int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
     if (!y) return KXW4_EARG;
     rc = check_act(a, w->K, w->scale_enc);
     if (rc) return rc;
-    if (a->T > 64 || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    if (a->T > kDecodeMaxT || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
     const int S = splits ? splits : kxw4_gemv_splits(w->M / 16);
     if (!valid_split(S)) return KXW4_ESHAPE;
-    SkinnyArgs args{};
-    args.count = 1;
-    args.w[0] = {w->codes, w->scales, y, w->M, S, 0, 0};
-    fill_act(args, a, w->group, w->scale_enc, y_dtype);
-    args.residual = residual;
-    args.variant = kVarGemv;
-    return launch_skinny(args, false, as_stream(stream));
+    const kxw4_weight_t *ws[1] = {w};
+    void *ys[1] = {y};
+    return decode_uniform(ws, ys, 1, a, y_dtype, residual, S, kVarGemv, as_stream(stream));
 }
 
 // kernels_dpas.cpp:947-967: -1 bad set, -2 non-uniform tier/K or missing
@@ -269,16 +283,10 @@ int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
     if (!a || !a->q || !a->scale || a->K != ws[0]->K) return KXW4_EPREP;
     const int rc = check_act(a, ws[0]->K, ws[0]->scale_enc);
     if (rc) return rc == KXW4_ESHAPE ? KXW4_EPREP : rc;
-    if (a->T > 64 || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    if (a->T > kDecodeMaxT || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
     const int S = kxw4_gemv_splits(groups);
     if (S > 16) return KXW4_ESPLIT;
-    SkinnyArgs args{};
-    args.count = count;
-    for (int i = 0; i < count; ++i)
-        args.w[i] = {ws[i]->codes, ws[i]->scales, ys[i], ws[i]->M, S, 0, 0};
-    fill_act(args, a, ws[0]->group, ws[0]->scale_enc, y_dtype);
-    args.variant = kVarFanout;
-    return launch_skinny(args, false, as_stream(stream));
+    return decode_uniform(ws, ys, count, a, y_dtype, nullptr, S, kVarFanout, as_stream(stream));
 }
 
 int kxw4_gemm(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,

@@ -63,7 +63,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     const int t0 = tt * BM;
 
     const int K = a.K, T = a.T, NT = K / kTileK, Nu = K / UNIT, G = K / a.group;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int gsh = __builtin_ctz(a.group / UNIT);       // unit -> scale group shift
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int n = lane & 15, g4 = lane >> 4;
 
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
         for (int jj = 0; jj < UPS; ++jj)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                raw[jj][j] = sb[j][(size_t)(((kb * UPS + jj) * UNIT) / a.group) * 16];
+                raw[jj][j] = sb[j][(size_t)((kb * UPS + jj) >> gsh) * 16];
     };
 
     uint16_t raw_cur[UPS][4], raw_nxt[UPS][4];

@@ -10,18 +10,17 @@ enum { kVarGemv = 0, kVarFanout = 1, kVarGemm = 2 };
 constexpr int kMaxWeights = 4;
 constexpr int kMaxSegments = 8;
 
-struct SkinnyWeight {
+struct DecodeWeight {
     const uint8_t *codes;
     const uint16_t *scales;
     void *y;
     int M;
-    int S;          // split count
-    int wrg;        // waves per row-group (set by the launcher)
-    int wg_begin;   // first work-group of this weight (set by the launcher)
+    int rg_begin;                     // first work-group (row-group) of this weight (set by the launcher)
+    int seg_split[kMaxSegments];      // split count per packed segment
 };
 
-struct SkinnyArgs {
-    SkinnyWeight w[kMaxWeights];
+struct DecodeArgs {
+    DecodeWeight w[kMaxWeights];
     int count;
     const int8_t *q;
     const float *ascale;
@@ -29,6 +28,11 @@ struct SkinnyArgs {
     const float *residual;
     int32_t *dbg;
     int T, K, group, block, scale_enc, y_bf16, variant;
+    int seg_count;
+    int seg_end[kMaxSegments];        // exclusive token end of each segment
+    int ts;                           // tokens per work-group slice (set by the launcher)
+    int smax;                         // largest split count of any token (set by the launcher)
+    int total_rg;                     // row-groups over all weights (set by the launcher)
 };
 
 struct GemmWeight {
@@ -70,7 +74,7 @@ int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T,
 int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 
-int launch_skinny(SkinnyArgs &a, bool debug, hipStream_t st);
+int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 
 }  // namespace kxw4

@@ -343,7 +343,8 @@ def test_packed_equals_serial(M, segments):
 
 @pytest.mark.parametrize("M,K,T,group,block,enc", [
     (4096, 4096, 1, 32, 32, 1), (5120, 17408, 1, 64, 32, 1), (512, 1024, 4, 64, 32, 1),
-    (64, 512, 2, 128, 0, 0), (48, 256, 1, 32, 32, 1), (16, 128, 1, 32, 32, 1)])
+    (64, 512, 2, 128, 0, 0), (48, 256, 1, 32, 32, 1), (16, 128, 1, 32, 32, 1),
+    (256, 2048, 50, 32, 32, 1), (128, 17408, 20, 64, 32, 1)])
 def test_gemv_reference_mode(M, K, T, group, block, enc):
     rng = np.random.default_rng(M * 3 + K)
     codes, scales = rand_weight(rng, M, K, group, enc)
@@ -380,7 +381,8 @@ def test_gemv_fanout(rows, T, block, enc, group):
 
 @pytest.mark.parametrize("M,K,T,block,enc,group,forced", [
     (17408 // 4, 5120, 8, 32, 1, 32, 0), (5120, 5120, 24, 32, 1, 64, 0), (1024, 2048, 128, 32, 1, 32, 0),
-    (5120, 5120, 8, 0, 0, 128, 16), (768, 4096, 200, 0, 0, 64, 0), (512, 2048, 40, 0, 0, 128, 0)])
+    (5120, 5120, 8, 0, 0, 128, 16), (768, 4096, 200, 0, 0, 64, 0), (512, 2048, 40, 0, 0, 128, 0),
+    (1024, 4096, 64, 32, 1, 32, 0), (256, 17408, 61, 0, 0, 64, 0)])
 def test_gemm_modes(M, K, T, block, enc, group, forced):
     rng = np.random.default_rng(M + T)
     codes, scales = rand_weight(rng, M, K, group, enc)
