@@ -29,6 +29,8 @@
 #include "kxw4_internal.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 namespace kxw4 {
 
@@ -50,16 +52,6 @@ struct DcStage {
 // code sum [nu][tl], then 64 dummy words.
 __host__ __device__ inline int decode_lds_words(int nu, int g, int tl, int smax, bool side) {
     return nu * tl * 16 + g * 8 + smax * tl * 16 + (side ? 2 * nu * tl : 0) + 64;
-}
-
-__device__ __forceinline__ v4i rotate8(v4i v) {
-    // DPP row_ror:8 -- lane i of each 16-lane row takes lane (i+8)%16
-    v4i r;
-    r.x = __builtin_amdgcn_mov_dpp(v.x, 0x128, 0xF, 0xF, false);
-    r.y = __builtin_amdgcn_mov_dpp(v.y, 0x128, 0xF, 0xF, false);
-    r.z = __builtin_amdgcn_mov_dpp(v.z, 0x128, 0xF, 0xF, false);
-    r.w = __builtin_amdgcn_mov_dpp(v.w, 0x128, 0xF, 0xF, false);
-    return r;
 }
 
 template <int AT, int UNIT, int MODE, bool DEBUG, int PFW>
@@ -324,6 +316,14 @@ static int launch_dc_unit(const DecodeArgs &a, int unit, int mode, bool debug, d
 }
 
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
+    // Up to 16 tokens with one split plan per weight go to the row-wave
+    // kernel. KXW4_DECODE_KERNEL=kparallel keeps them here (used by the tests
+    // to cover this kernel at small T).
+    const char *force = getenv("KXW4_DECODE_KERNEL");
+    if (!debug && !(force && strcmp(force, "kparallel") == 0)) {
+        const int r = launch_rowwave(a, st);
+        if (r != 1) return r;
+    }
     constexpr size_t kBudget = 64 * 1024;
     const int unit = a.block == 32 ? 32 : a.group;
     const int nu = a.K / unit, g = a.K / a.group;

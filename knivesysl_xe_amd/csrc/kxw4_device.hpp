@@ -75,6 +75,35 @@ __device__ __forceinline__ int sext4(uint32_t v) {
     return z >= 8 ? z - 16 : z;
 }
 
+// DPP row_ror:8 -- lane i of each 16-lane row takes lane (i+8)%16.
+__device__ __forceinline__ v4i rotate8(v4i v) {
+    v4i r;
+    r.x = __builtin_amdgcn_mov_dpp(v.x, 0x128, 0xF, 0xF, false);
+    r.y = __builtin_amdgcn_mov_dpp(v.y, 0x128, 0xF, 0xF, false);
+    r.z = __builtin_amdgcn_mov_dpp(v.z, 0x128, 0xF, 0xF, false);
+    r.w = __builtin_amdgcn_mov_dpp(v.w, 0x128, 0xF, 0xF, false);
+    return r;
+}
+
+// Barrier for LDS traffic only: waits for this wave's LDS accesses, not for
+// its outstanding global loads, so a prefetch ring stays in flight.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Barrier after direct global->LDS loads: the caller has already waited for
+// them with an explicit vmcnt (they were issued before the loads still in
+// flight); this waits for the wave's own LDS accesses and synchronises. The
+// empty asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_sync_after_dma() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0); vmcnt, expcnt untouched
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Byte offset of element k inside its 64-element activation chunk.
 __host__ __device__ __forceinline__ int act_slot(int k) {
     return 16 * ((k >> 3) & 3) + 8 * ((k >> 5) & 1) + (k & 7);

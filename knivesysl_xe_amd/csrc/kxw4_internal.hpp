@@ -17,6 +17,8 @@ struct DecodeWeight {
     int M;
     int rg_begin;                     // first work-group (row-group) of this weight (set by the launcher)
     int seg_split[kMaxSegments];      // split count per packed segment
+    int wg_begin;                     // row-wave kernel: first work-group of this weight
+    int wrg;                          // row-wave kernel: waves per row-group
 };
 
 struct DecodeArgs {
@@ -75,6 +77,8 @@ int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, 
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
+// Returns 1 (nothing launched) when the shape is outside the row-wave kernel's range.
+int launch_rowwave(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 
 }  // namespace kxw4

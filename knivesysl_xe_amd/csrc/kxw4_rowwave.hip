@@ -1,0 +1,320 @@
+// kxw4_rowwave.hip — decode-shaped projections for up to 16 tokens with one
+// split plan for all tokens of a weight: the GEMV (kernels_dpas.cpp:586-675),
+// the fan-out GEMV (945-1102) and the batched GEMM at small T (1334-1490).
+//
+// Each wave owns one (row-group, split). It streams the split's 1 KB weight
+// tiles through a ring of PF loads in flight and runs the split's reference
+// chain in registers: the int8 MFMA leaves row n of tokens 4*(l/16)+r in
+// register r of lane l for every unit, so a lane's four accumulators are four
+// of the reference's chains, fed unit by unit in order. The waves of one
+// row-group take consecutive splits (a work-group holds 8 / min(S, 8)
+// row-groups); with S > 1 the split partials meet in LDS and one wave adds
+// them in split order starting from 0.0f.
+//
+// The activations (T x K int8) and the work-group's FP16 scales are staged
+// into LDS once per work-group with direct global->LDS loads, so the
+// weight-tile load is the only vector-memory instruction of the streaming
+// loop. Activation rows are padded by 16 bytes, so the 8 or 16 token rows a
+// 16-lane quarter reads fall on distinct banks, and every LDS address in the
+// loop is a per-ring base plus an immediate offset. Whole rings run without
+// predicates; only a split's last, partial ring selects the old accumulator
+// for its padded positions.
+#include "kxw4_device.hpp"
+#include "kxw4_internal.hpp"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace kxw4 {
+
+constexpr int kRwWaves = 8;
+constexpr int kRwThreads = 64 * kRwWaves;
+constexpr size_t kRwLdsMax = 64 * 1024;
+
+template <int TT, int UNIT, int MODE, bool ALT2, int PF>
+__global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs a) {
+    constexpr int UPS = kTileK / UNIT;
+    static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+    int wi = 0;
+    for (int i = 1; i < a.count; ++i)
+        if ((int)blockIdx.x >= a.w[i].wg_begin) wi = i;
+    const DecodeWeight &W = a.w[wi];
+    const int S = W.seg_split[0], wrg = W.wrg, R = kRwWaves / wrg;
+    const int K = a.K, T = a.T, M = W.M;
+    const int NT = K / kTileK, Nu = K / UNIT, G = K / a.group;
+    const int gsh = __builtin_ctz(a.group / UNIT);
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, n = lane & 15, g4 = lane >> 4;
+    const int rgl = wave / wrg, wj = wave - rgl * wrg;
+    const int rg0 = ((int)blockIdx.x - W.wg_begin) * R;      // first row-group of the work-group
+    const int nrg = min(R, M / 16 - rg0);                     // row-groups it owns
+    const bool active = rgl < nrg;
+    const int rg = rg0 + (active ? rgl : 0);
+
+    const int pitch = K + 16;                                 // padded activation row
+    int8_t *Act = reinterpret_cast<int8_t *>(smem);
+    uint16_t *Sc = reinterpret_cast<uint16_t *>(smem + (size_t)T * pitch);
+    float *Asc = reinterpret_cast<float *>(Sc + R * G * 16);
+    int *Zs = reinterpret_cast<int *>(Asc + (MODE != 0 ? Nu * 16 : 0));
+    float *Part = reinterpret_cast<float *>(Zs + (MODE != 0 ? Nu * 16 : 0));
+    // 16 zero words: the scale (and activation scale) read of a padded
+    // position, so its chain step fma(p, 0, acc) leaves acc unchanged
+    // (p is a finite integer and a chain that starts at +0 never holds -0)
+    float *Zero = Part + (S > 1 ? R * S * 256 : 0);
+
+    // ---- stage activations and scales with direct global->LDS loads ----
+    // LDS chunk x (16 bytes) is chunk x % (kc+1) of activation row x / (kc+1)
+    // (the last chunk of a row is padding), then the work-group's scales.
+    const int kc = K / 16;
+    const int act_chunks = T * (kc + 1);
+    const int total = act_chunks + nrg * G * 2;
+    for (int c0 = wave * 64; c0 < total; c0 += kRwThreads) {
+        const int x = c0 + lane;
+        if (x < total) {
+            const void *src;
+            if (x < act_chunks) {
+                const int t = x / (kc + 1), p = x - t * (kc + 1);
+                src = a.q + (size_t)t * K + 16 * min(p, kc - 1);
+            } else {
+                src = W.scales + (size_t)rg0 * G * 16 + (size_t)(x - act_chunks) * 8;
+            }
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(smem + (size_t)c0 * 16),
+                                             16, 0, 0);
+        }
+    }
+
+    // ---- the wave's first split and its ring ----
+    const int sb = wj * S / wrg, se = (wj + 1) * S / wrg;
+    int u0 = (int)((long long)Nu * sb / S), u1 = (int)((long long)Nu * (sb + 1) / S);
+    int kt0 = u0 / UPS, ntw = (u1 + UPS - 1) / UPS - kt0;
+    const v4u *wrow = reinterpret_cast<const v4u *>(W.codes + (size_t)rg * NT * kTileBytes) + lane;
+    v4u ring[PF];
+    // tile i of the current split; an empty split (more splits than units)
+    // or an idle wave reads a valid tile it never uses
+    auto load = [&](int i) { return wrow[(size_t)min(kt0 + max(i, 0), NT - 1) * (kTileBytes / 16)]; };
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PF; ++p) ring[p] = load(min(p, ntw - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    // the staging loads were issued before the PF ring loads and complete first
+    __builtin_amdgcn_s_waitcnt(0x0F70 | PF);
+    const bool ref_block = a.block == 32, zp = a.scale_enc == 1;
+    if (MODE != 0) {
+        // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
+        for (int x = tid; x < Nu * 16; x += kRwThreads) {
+            const int u = x >> 4, t = min(x & 15, T - 1);
+            Asc[x] = ref_block ? a.ascale[(size_t)t * (K / 32) + u] : 1.0f;
+            int sm = 0;
+            if (zp)
+                for (int q = (u * UNIT) / 32; q < ((u + 1) * UNIT) / 32; ++q)
+                    sm += a.asum[(size_t)t * (K / 32) + q];
+            Zs[x] = sm;
+        }
+    }
+    if (tid < 16) Zero[tid] = 0.0f;
+    lds_sync_after_dma();
+
+    // ---- streaming: one chain per split, in registers ----
+    const bool gemm_var = a.variant == kVarGemm;
+    // this lane's activation row (MFMA row n; with up to 8 tokens rows 8-15
+    // repeat rows 0-7 and are never stored) and its K-slot group
+    const int ta = TT == 8 ? min(n & 7, T - 1) : min(n, T - 1);
+    const int8_t *abase = Act + (size_t)ta * pitch + 16 * g4;
+    const uint16_t *sbase = Sc + rgl * G * 16 + n;
+    float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (active) {
+        for (int s = sb; s < se; ++s) {
+            if (s != sb) {
+                u0 = (int)((long long)Nu * s / S);
+                u1 = (int)((long long)Nu * (s + 1) / S);
+                kt0 = u0 / UPS;
+                ntw = (u1 + UPS - 1) / UPS - kt0;
+#pragma unroll
+                for (int p = 0; p < PF; ++p) ring[p] = load(min(p, ntw - 1));
+            }
+            float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+            // One ring of PF tiles starting at tile ib of the split. PRED
+            // marks the rings that may hold padded positions or units outside
+            // the split.
+            auto ring_pass = [&](int ib, auto pred) {
+                constexpr bool PRED = decltype(pred)::value;
+                const int8_t *ar = abase + (size_t)(kt0 + ib) * kTileK;
+                const uint16_t *sr = sbase + (MODE == 0 ? (size_t)(kt0 + ib) * UPS * 16 : 0);
+#pragma unroll
+                for (int p = 0; p < PF; ++p) {
+                    const int i = ib + p;
+                    const int kb = kt0 + i;
+                    const v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
+                    const v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
+                    const v4u wd = ring[p];
+#pragma unroll
+                    for (int j = 0; j < UPS; ++j) {
+                        const int u = kb * UPS + j;
+                        const bool in = !PRED || (i < ntw && (UNIT == 128 || (u >= u0 && u < u1)));
+                        const v4i zero = {0, 0, 0, 0};
+                        v4i acc;
+                        if constexpr (UNIT == 128) {
+                            acc = mfma_k64(A0, unpack_k64(wd.x, wd.y), zero);
+                            acc = mfma_k64(A1, unpack_k64(wd.z, wd.w), acc);
+                        } else if constexpr (UNIT == 64) {
+                            acc = j == 0 ? mfma_k64(A0, unpack_k64(wd.x, wd.y), zero)
+                                         : mfma_k64(A1, unpack_k64(wd.z, wd.w), zero);
+                        } else {
+                            const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
+                            const v4i c = j < 2 ? A0 : A1;
+                            const long av = (j & 1) ? (long)(((uint64_t)(uint32_t)c.w << 32) | (uint32_t)c.z)
+                                                    : (long)(((uint64_t)(uint32_t)c.y << 32) | (uint32_t)c.x);
+                            acc = mfma_k32(av, unpack_k32(d), zero);
+                        }
+                        // MODE 0 has unit == group, so unit u reads scale u
+                        const uint16_t *sp = MODE == 0 ? &sr[(p * UPS + j) * 16] : &sbase[(u >> gsh) * 16];
+                        const uint32_t sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
+                        // GEMV: units at odd offsets from the split start feed the
+                        // second accumulator. With an even ring and an even number
+                        // of units per tile the parity is fixed by p (whole-tile
+                        // units) or j; when the split starts on an odd unit the two
+                        // accumulators trade roles, and their final sum commutes.
+                        float *F = (ALT2 && (UNIT == 128 ? (p & 1) : (j & 1))) ? f1 : f0;
+                        if constexpr (MODE == 0) {
+                            const float w = half_bits_to_float((uint16_t)sv);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float nf = __builtin_fmaf((float)acc[r], w, F[r]);
+                                F[r] = nf;
+                            }
+                        } else {
+                            const float w = half_bits_to_float(zp ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
+                            const int z = sext4(sv);
+                            const v4i zv = *reinterpret_cast<const v4i *>(Zs + u * 16 + 4 * g4);
+                            const float4 av = *reinterpret_cast<const float4 *>(in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4);
+                            const float avr[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                int pv = acc[r];
+                                if (zp) pv -= (z * zv[r]) << 4;
+                                const float pf = (float)pv;
+                                float nf;
+                                if (!ref_block) nf = __builtin_fmaf(pf, w, F[r]);
+                                else if (gemm_var) nf = __builtin_fmaf(pf, w * avr[r], F[r]);
+                                else nf = __builtin_fmaf(pf * w, avr[r], F[r]);
+                                F[r] = nf;
+                            }
+                        }
+                    }
+                    ring[p] = load(min(i + PF, ntw - 1));
+                    // keep each slot's unpack behind the previous slot's load, so
+                    // the wait before it covers only that slot
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+
+            // whole rings run unpredicated when the split starts and ends on
+            // tile boundaries; the rest (at most one ring then) is predicated
+            const bool aligned = u0 % UPS == 0 && u1 % UPS == 0;
+            int ib = 0;
+            if (aligned)
+                for (; ib + PF <= ntw; ib += PF) ring_pass(ib, std::false_type{});
+            for (; ib < ntw; ib += PF) ring_pass(ib, std::true_type{});
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = ALT2 ? f0[r] + f1[r] : f0[r];
+                if (S > 1) Part[((rgl * S + s) * 4 + r) * 64 + lane] = v;
+                else res[r] = v;
+            }
+        }
+    }
+
+    // ---- ordered split sum and output ----
+    if (S > 1) {
+        lds_sync();
+        if (!active || wj != 0) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float sum = 0.0f;
+            for (int s = 0; s < S; ++s) sum = sum + Part[((rgl * S + s) * 4 + r) * 64 + lane];
+            res[r] = sum;
+        }
+    } else if (!active) {
+        return;
+    }
+    const int row = rg * 16 + n;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int t = 4 * g4 + r;
+        if (t >= T) continue;
+        const float v = a.block == 0 ? res[r] * (a.ascale[t] * 0.0625f) : res[r] * 0.0625f;
+        float out;
+        if (a.residual) out = v + a.residual[(size_t)t * M + row];
+        else if (ALT2 && S > 1) out = v + 0.0f;
+        else out = v;
+        if (a.y_bf16) static_cast<uint16_t *>(W.y)[(size_t)t * M + row] = float_to_bf16(out);
+        else static_cast<float *>(W.y)[(size_t)t * M + row] = out;
+    }
+}
+
+template <int TT, int UNIT, int MODE, bool ALT2, int PF>
+static int rw_launch(const DecodeArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((rowwave_kernel<TT, UNIT, MODE, ALT2, PF>), grid, dim3(kRwThreads), lds, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// pf8: the longest split streams enough tiles for a deeper ring (plain
+// per-token mode only; the general mode keeps 4)
+template <int TT, int UNIT>
+static int rw_mode(const DecodeArgs &a, int mode, bool pf8, dim3 grid, size_t lds, hipStream_t st) {
+    const bool alt2 = a.variant == kVarGemv;
+    if (mode == 0) {
+        if (pf8)
+            return alt2 ? rw_launch<TT, UNIT, 0, true, 8>(a, grid, lds, st)
+                        : rw_launch<TT, UNIT, 0, false, 8>(a, grid, lds, st);
+        return alt2 ? rw_launch<TT, UNIT, 0, true, 4>(a, grid, lds, st)
+                    : rw_launch<TT, UNIT, 0, false, 4>(a, grid, lds, st);
+    }
+    return alt2 ? rw_launch<TT, UNIT, 1, true, 4>(a, grid, lds, st)
+                : rw_launch<TT, UNIT, 1, false, 4>(a, grid, lds, st);
+}
+
+template <int TT>
+static int rw_unit(const DecodeArgs &a, int unit, int mode, bool pf8, dim3 grid, size_t lds,
+                   hipStream_t st) {
+    if (unit == 128) return rw_mode<TT, 128>(a, mode, pf8, grid, lds, st);
+    if (unit == 64) return rw_mode<TT, 64>(a, mode, pf8, grid, lds, st);
+    return rw_mode<TT, 32>(a, mode, pf8, grid, lds, st);
+}
+
+int launch_rowwave(DecodeArgs &a, hipStream_t st) {
+    if (a.T < 1 || a.T > 16) return 1;
+    const int unit = a.block == 32 ? 32 : a.group;
+    const int nu = a.K / unit, g = a.K / a.group;
+    const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
+    int wg = 0, rmax = 1, part = 0, tiles = 0;
+    for (int i = 0; i < a.count; ++i) {
+        DecodeWeight &w = a.w[i];
+        const int S = w.seg_split[0];
+        for (int s = 1; s < a.seg_count; ++s)
+            if (w.seg_split[s] != S) return 1;
+        if (S < 1 || S > 16) return 1;
+        w.wrg = std::min(S, kRwWaves);
+        const int R = kRwWaves / w.wrg;
+        w.wg_begin = wg;
+        wg += (w.M / 16 + R - 1) / R;
+        rmax = std::max(rmax, R);
+        if (S > 1) part = std::max(part, R * S);
+        tiles = std::max(tiles, (a.K / kTileK + S - 1) / S);
+    }
+    const size_t act = (size_t)a.T * (a.K + 16);
+    const size_t scales = (size_t)rmax * g * 32;
+    const size_t lds = act + scales + (mode != 0 ? (size_t)2 * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
+    if (lds > kRwLdsMax) return 1;
+    const dim3 grid(wg);
+    const bool pf8 = tiles >= 16;
+    if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, lds, st);
+    return rw_unit<16>(a, unit, mode, pf8, grid, lds, st);
+}
+
+}  // namespace kxw4

@@ -299,6 +299,18 @@ def test_baseline_cfg4_row_subset():
     run_config("cfg4", rows=[(0, 512), (8192, 8704), (16896, 17408)])
 
 
+@pytest.fixture
+def kparallel(monkeypatch):
+    # up to 16 tokens normally run on the row-wave kernel; this keeps the
+    # K-parallel decode kernel covered at the decode configurations
+    monkeypatch.setenv("KXW4_DECODE_KERNEL", "kparallel")
+
+
+@pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
+def test_baseline_config_kparallel(name, kparallel):
+    run_config(name)
+
+
 # ------------------------------------------------------------------ properties
 @pytest.mark.parametrize("kind", ["gemm", "gemv"])
 def test_row_independence_specwave(kind):
@@ -344,7 +356,8 @@ def test_packed_equals_serial(M, segments):
 @pytest.mark.parametrize("M,K,T,group,block,enc", [
     (4096, 4096, 1, 32, 32, 1), (5120, 17408, 1, 64, 32, 1), (512, 1024, 4, 64, 32, 1),
     (64, 512, 2, 128, 0, 0), (48, 256, 1, 32, 32, 1), (16, 128, 1, 32, 32, 1),
-    (256, 2048, 50, 32, 32, 1), (128, 17408, 20, 64, 32, 1)])
+    (256, 2048, 50, 32, 32, 1), (128, 17408, 20, 64, 32, 1), (2048, 2048, 13, 64, 32, 1),
+    (1024, 4096, 5, 128, 0, 0), (64, 512, 16, 64, 0, 0)])
 def test_gemv_reference_mode(M, K, T, group, block, enc):
     rng = np.random.default_rng(M * 3 + K)
     codes, scales = rand_weight(rng, M, K, group, enc)
@@ -382,7 +395,8 @@ def test_gemv_fanout(rows, T, block, enc, group):
 @pytest.mark.parametrize("M,K,T,block,enc,group,forced", [
     (17408 // 4, 5120, 8, 32, 1, 32, 0), (5120, 5120, 24, 32, 1, 64, 0), (1024, 2048, 128, 32, 1, 32, 0),
     (5120, 5120, 8, 0, 0, 128, 16), (768, 4096, 200, 0, 0, 64, 0), (512, 2048, 40, 0, 0, 128, 0),
-    (1024, 4096, 64, 32, 1, 32, 0), (256, 17408, 61, 0, 0, 64, 0)])
+    (1024, 4096, 64, 32, 1, 32, 0), (256, 17408, 61, 0, 0, 64, 0), (4096, 5120, 16, 0, 0, 128, 0),
+    (1024, 4096, 12, 32, 1, 32, 0), (2048, 2048, 5, 32, 1, 64, 4), (512, 1024, 3, 0, 0, 64, 8)])
 def test_gemm_modes(M, K, T, block, enc, group, forced):
     rng = np.random.default_rng(M + T)
     codes, scales = rand_weight(rng, M, K, group, enc)
