@@ -129,14 +129,31 @@ def check_against_oracle(cfg, inp, outs, rows=512):
     return True
 
 
-def measure(cfg, steps, warmup):
+def time_eager(run, copies, steps, warmup):
+    """Back-to-back eager launches bracketed by events on the launch stream
+    (for counter collection, which wants one dispatch per launch)."""
+    import torch
+    for i in range(max(warmup, 1)):
+        run(copies[i % len(copies)])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        run(copies[(warmup + i) % len(copies)])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3, time.perf_counter() - t0
+
+
+def measure(cfg, steps, warmup, eager=False):
     import torch
     inp, ws, x, act = setup(cfg)
     dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
     outs = [torch.empty(cfg.tokens, w.M, dtype=dt, device="cuda") for w in ws]
     run = launcher(cfg, act, outs)
     copies, rot_bytes = make_copies(ws)
-    secs, wall = time_graph(run, copies, steps, warmup)
+    secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
     run(copies[0])
     torch.cuda.synchronize()
     exact = check_against_oracle(cfg, inp, outs)
@@ -192,8 +209,23 @@ def cpu_baseline(cfg, budget_s=10.0):
                       "scalar C++ oracle, OpenMP over output rows"}
 
 
+def calibration_copy(mib):
+    """A device-to-device copy of `mib` MiB: the known-size kernel the
+    FETCH_SIZE / WRITE_SIZE counters are calibrated against."""
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy: 3 x {mib} MiB")
+
+
 def read_traffic(name):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any:
+    fetch_kib * fetch_cal + write_kib * write_cal, where each factor is the
+    known size of a plain copy over what the same counter read for it."""
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
     if not os.path.exists(path):
         return None
@@ -206,7 +238,7 @@ def read_traffic(name):
             except ValueError:
                 pass
     try:
-        return int((vals["fetch_kib"] + vals["write_kib"]) * 1024 * vals["calibration"])
+        return int((vals["fetch_kib"] * vals["fetch_cal"] + vals["write_kib"] * vals["write_cal"]) * 1024)
     except KeyError:
         return None
 
@@ -220,6 +252,10 @@ def main():
                     help="extra BASELINE configs to report ('' for none)")
     ap.add_argument("--extra-steps", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of a graph replay (for counter runs)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run a device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -231,16 +267,18 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     head = workloads.CONFIGS["cfg1"]
     log(f"headline {head.note}")
-    r = measure(head, args.steps, args.warmup)
+    r = measure(head, args.steps, args.warmup, args.eager)
     log(f"cfg1: {r['kernel_us']:.2f} us/launch, {r['GBps']:.1f} GB/s, exact={r['bit_exact_vs_oracle_rows0_512']}")
     extra = {}
     for name in [c for c in args.configs.split(",") if c]:
         cfg = workloads.CONFIGS[name]
         log(f"{name}: {cfg.note}")
-        extra[name] = measure(cfg, args.extra_steps, 5)
+        extra[name] = measure(cfg, args.extra_steps, 5, args.eager)
         e = extra[name]
         log(f"{name}: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, {e['TOPS']:.1f} TOPS, "
             f"frac {e['roofline_frac']:.3f}, exact={e['bit_exact_vs_oracle_rows0_512']}")
+    if args.copy_mib:
+        calibration_copy(args.copy_mib)
     log("cpu baseline (oracle on host cores)")
     cpu = cpu_baseline(head, args.cpu_budget)
     per = r["kernel_us"] / 1e6

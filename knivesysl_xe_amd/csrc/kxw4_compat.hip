@@ -1,0 +1,200 @@
+// kxw4_compat.hip — the reference's C++ projection functions
+// (xpu/src/tq_common.hpp:385-461) as shims over the C ABI. Host code only.
+#include <hip/hip_runtime.h>
+
+#include "../../include/kxw4_compat.hpp"
+
+namespace {
+
+hipStream_t g_stream = nullptr;
+
+void dfree(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+// Prepared single-token activation: the counterpart of the reference's
+// library-global grow-only scratch (kernels_dpas.cpp:133-149).
+struct Prepared {
+    int8_t *q = nullptr;
+    float *scale = nullptr;
+    int32_t *sum = nullptr;
+    int cap = 0;      // capacity in K
+    int K = 0;        // K of the last prepare (0 = none)
+} g_act;
+
+bool ensure_act(int K) {
+    if (K <= g_act.cap) return true;
+    dfree(g_act.q);
+    dfree(g_act.scale);
+    dfree(g_act.sum);
+    g_act = Prepared{};
+    if (hipMalloc(&g_act.q, (size_t)K) != hipSuccess ||
+        hipMalloc(&g_act.scale, (size_t)(K / 32) * sizeof(float)) != hipSuccess ||
+        hipMalloc(&g_act.sum, (size_t)(K / 32) * sizeof(int32_t)) != hipSuccess) {
+        dfree(g_act.q);
+        dfree(g_act.scale);
+        dfree(g_act.sum);
+        g_act = Prepared{};
+        return false;
+    }
+    g_act.cap = K;
+    return true;
+}
+
+kxw4_weight_t w4_of(const tq_qmma_weight_t *w) {
+    kxw4_weight_t d;
+    d.M = w->M;
+    d.K = w->K;
+    d.group = w->s4_k64 ? 64 : 32;
+    d.scale_enc = KXW4_SCALE_FP16_ZP4;
+    d.codes = w->d_s4;
+    d.scales = w->d_s4_scale;
+    return d;
+}
+
+kxw4_act_t prepared_act() {
+    kxw4_act_t a;
+    a.T = 1;
+    a.K = g_act.K;
+    a.block = 32;
+    a.q = g_act.q;
+    a.scale = g_act.scale;
+    a.sum = g_act.sum;
+    return a;
+}
+
+bool w4_ready(const tq_qmma_weight_t *w) {
+    return w && w->s4_ready && !w->s4_k16 && w->d_s4 && w->d_s4_scale;
+}
+
+}  // namespace
+
+extern "C" void kxw4_compat_set_stream(void *stream) { g_stream = static_cast<hipStream_t>(stream); }
+
+int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode) {
+    if (!w || !w->d_A || !w->d_block_scale_inv || !w->block_scaled || !w->e2m3) return -1;
+    if (w->M % 16 || w->K % 128) return -2;
+    if (mode == 2 && (w->Kt & 1)) return -3;
+    if (mode != 0 && mode != 2) return KXW4_ETIER;
+    const int group = mode == 2 ? 64 : 32;
+    uint8_t *codes = nullptr;
+    uint16_t *scales = nullptr;
+    if (hipMalloc(&codes, kxw4_code_bytes(w->M, w->K)) != hipSuccess) return KXW4_EHIP;
+    if (hipMalloc(&scales, kxw4_scale_count(w->M, w->K, group) * sizeof(uint16_t)) != hipSuccess) {
+        dfree(codes);
+        return KXW4_EHIP;
+    }
+    int rc = kxw4_repack_e2m3(w->d_A, w->d_block_scale_inv, w->scale_cols, w->M, w->K, mode, codes,
+                              scales, g_stream);
+    if (rc == 0 && hipStreamSynchronize(g_stream) != hipSuccess) rc = KXW4_EHIP;
+    if (rc != 0) {
+        dfree(codes);
+        dfree(scales);
+        return rc;
+    }
+    dfree(w->d_A);
+    dfree(w->d_block_scale_inv);
+    w->d_A = nullptr;
+    w->d_block_scale_inv = nullptr;
+    w->d_s4 = codes;
+    w->d_s4_scale = scales;
+    w->s4_k16 = 0;
+    w->s4_k64 = mode == 2 ? 1 : 0;
+    w->s4_ready = 1;
+    return 0;
+}
+
+int x_w4_repack_weight(tq_qmma_weight_t *w) { return x_w4_repack_weight_mode(w, 0); }
+
+void x_quantize_act_s8(const float *d_x, int K, int8_t *d_q, float *d_scale, int32_t *d_sum) {
+    kxw4_quantize_act(d_x, KXW4_F32, 1, K, 32, d_q, d_scale, d_sum, g_stream);
+}
+
+void x_prepare_gemv_act_s8(const float *d_x, int K) {
+    if (!d_x || K <= 0 || K % 128 || !ensure_act(K)) return;
+    if (kxw4_quantize_act(d_x, KXW4_F32, 1, K, 32, g_act.q, g_act.scale, g_act.sum, g_stream) == 0)
+        g_act.K = K;
+}
+
+void x_silu_mul_quant(float *d_out, const float *d_gate, const float *d_up, int K) {
+    if (!d_gate || !d_up || K <= 0 || K % 128 || !ensure_act(K)) return;
+    if (kxw4_silu_mul_quant(d_out, d_gate, d_up, 1, K, 32, g_act.q, g_act.scale, g_act.sum,
+                            g_stream) == 0)
+        g_act.K = K;
+}
+
+void x_rmsnorm_quant(float *d_out, const float *d_in, const uint16_t *d_w, int H, float eps) {
+    if (!d_in || !d_w || H <= 0 || H % 128 || !ensure_act(H)) return;
+    if (kxw4_rmsnorm_quant(d_out, d_in, d_w, 1, H, eps, 32, g_act.q, g_act.scale, g_act.sum,
+                           g_stream) == 0)
+        g_act.K = H;
+}
+
+int x_gemv_w4a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual) {
+    if (!w4_ready(w) || !d_y) return -1;
+    if (g_act.K != w->K) return -2;
+    const kxw4_weight_t d = w4_of(w);
+    const kxw4_act_t a = prepared_act();
+    return kxw4_gemv(&d, &a, d_y, KXW4_F32, d_residual, 0, g_stream);
+}
+
+int x_gemv_w4a8(const tq_qmma_weight_t *w, const float *d_x, float *d_y) {
+    if (!w || !d_x) return -1;
+    x_prepare_gemv_act_s8(d_x, w->K);
+    return x_gemv_w4a8_prepared(w, d_y, nullptr);
+}
+
+int x_gemv_w4a8_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y) {
+    if (!w || !d_x || !d_residual) return -1;
+    x_prepare_gemv_act_s8(d_x, w->K);
+    return x_gemv_w4a8_prepared(w, d_y, d_residual);
+}
+
+int x_gemv_w4a8_fanout(const tq_qmma_weight_t *const *ws, float *const *ys, int count) {
+    if (!ws || !ys || count <= 0 || count > 4) return -1;
+    kxw4_weight_t d[4];
+    const kxw4_weight_t *dp[4];
+    void *yp[4];
+    for (int i = 0; i < count; ++i) {
+        const tq_qmma_weight_t *w = ws[i];
+        if (!w4_ready(w) || !ys[i] || w->K != ws[0]->K || w->M % 16 || w->s4_k64 != ws[0]->s4_k64)
+            return -2;
+        d[i] = w4_of(w);
+        dp[i] = &d[i];
+        yp[i] = ys[i];
+    }
+    if (g_act.K != ws[0]->K) return -3;
+    const kxw4_act_t a = prepared_act();
+    return kxw4_gemv_fanout(dp, yp, count, &a, KXW4_F32, g_stream);
+}
+
+void x_quantize_act_chunk(const float *d_x, int K, int T, int8_t *d_aq, float *d_as, int32_t *d_asum) {
+    kxw4_quantize_act(d_x, KXW4_F32, T, K, 32, d_aq, d_as, d_asum, g_stream);
+}
+
+int x_gemm_w4a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as,
+                const int32_t *d_asum, float *d_y, int T, const int *offsets, int segments) {
+    if (!w4_ready(w) || !d_aq || !d_as || !d_asum || !d_y) return -1;
+    const kxw4_weight_t d = w4_of(w);
+    kxw4_act_t a;
+    a.T = T;
+    a.K = w->K;
+    a.block = 32;
+    a.q = d_aq;
+    a.scale = d_as;
+    a.sum = d_asum;
+    return kxw4_gemm(&d, &a, d_y, KXW4_F32, nullptr, offsets, segments, 0, g_stream);
+}
+
+int x_gemv_qmma_prepared(const tq_qmma_weight_t *w, const float *d_x, float *d_y,
+                         const float *d_residual) {
+    if (!w || !d_x || !d_y) return -1;
+    if (w->s4_ready) return x_gemv_w4a8_prepared(w, d_y, d_residual);
+    return KXW4_ETIER;
+}
+
+int x_gemv_qmma_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y) {
+    if (!w || !d_x || !d_residual || !d_y) return -1;
+    if (w->s4_ready) return x_gemv_w4a8_add(w, d_x, d_residual, d_y);
+    return KXW4_ETIER;
+}

@@ -18,6 +18,32 @@
  *                    128, plain FP16 scale, zero point 0 (ORC_SCALE_FP16).
  * The int32 "unit" partial is taken over min(weight group, activation block);
  * it is exact in every mode.
+ *
+ * Pinning (what checks each function against something other than itself):
+ *   conversions      numpy IEEE RNE, all 65536 FP16 codes, BF16 ties
+ *   quantizers       golden vectors written from numpy (the reference's
+ *                    chunk_quant_bench edge pattern), round-half-even ties
+ *   partials         numpy int64 matrix products
+ *   projection       exact-rational cases, hand-derived accumulation-order
+ *                    cases per variant, all-ones => K, GEMM-vs-GEMV cosine gate
+ *   split plans      the reference's stated values for the BASELINE shapes
+ *   orc_e2m3         the OCP FP6 E2M3 closed form
+ *   orc_e2m3_code_at parity unpinned beyond structure: tests show every
+ *                    (row, col) owns a distinct contiguous 6-bit field of its
+ *                    384-byte tile; the bit positions themselves restate
+ *                    kernels_core.cpp:46-75 and no reference vector checks them
+ *   orc_fit_int4_asym parity unpinned beyond known answers and invariants
+ *                    (exact fits of evenly spaced groups, zero kept, nibble
+ *                    reserved, codes within half a step); the least-squares
+ *                    refinement's rounding on general inputs restates
+ *                    kernels_dpas.cpp:229-256 unchecked
+ *   contract         selects how a chain step `acc += x*y` (and the fit's
+ *                    least-squares sums) round: 1 = one fused multiply-add,
+ *                    what icpx's default contraction makes of the
+ *                    reference's source and what the HIP kernels implement;
+ *                    0 = separate multiply and add, the literal source. Both
+ *                    are restated; which one Intel's compiled reference
+ *                    produces is parity unpinned (no reference output pins it)
  */
 #ifndef W4A8_ORACLE_H
 #define W4A8_ORACLE_H
