@@ -24,6 +24,9 @@
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace kxw4 {
 
 constexpr int kGemmThreads = 256;
@@ -349,6 +352,13 @@ static void launch_wm_unit(const GemmArgs &a, int mode, bool splits, bool debug,
 }
 
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
+    // The per-token, one-split mode goes to the LDS-DMA kernel;
+    // KXW4_GEMM_KERNEL=general keeps it here (the tests cover both).
+    const char *force = getenv("KXW4_GEMM_KERNEL");
+    if (!debug && !(force && strcmp(force, "general") == 0)) {
+        const int r = launch_gemm2(a, st);
+        if (r != 1) return r;
+    }
     bool splits = false;
     int nt = 0;
     for (int i = 0; i < a.count; ++i) {

@@ -80,5 +80,7 @@ int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) when the shape is outside the row-wave kernel's range.
 int launch_rowwave(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
+// Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
+int launch_gemm2(GemmArgs &a, hipStream_t st);
 
 }  // namespace kxw4

@@ -311,6 +311,22 @@ def test_baseline_config_kparallel(name, kparallel):
     run_config(name)
 
 
+@pytest.fixture
+def gemm_general(monkeypatch):
+    # the per-token prefill shapes normally run on the LDS-DMA GEMM kernel;
+    # this keeps the general GEMM kernel covered on them
+    monkeypatch.setenv("KXW4_GEMM_KERNEL", "general")
+
+
+@pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
+def test_baseline_config_gemm_general(name, gemm_general):
+    run_config(name)
+
+
+def test_baseline_cfg4_rows_gemm_general(gemm_general):
+    run_config("cfg4", rows=[(0, 256), (17152, 17408)])
+
+
 # ------------------------------------------------------------------ properties
 @pytest.mark.parametrize("kind", ["gemm", "gemv"])
 def test_row_independence_specwave(kind):
