@@ -3,12 +3,17 @@
 // 1255-1332, 1334-1490) with one split per token, on int8 MFMA.
 //
 // Block tile BM tokens x 128 output rows (8 row-groups), 4 waves in a 2 x 2
-// grid, wave tile BM/2 tokens x 64 rows. Per 128-K step both operands reach
-// LDS through direct global->LDS loads (no staging registers, no LDS store
-// instructions), double-buffered: the loads of step k+1 are issued right
-// after the barrier that opens step k. Activation rows are XOR-swizzled on
-// the load side so a 16-lane quarter of an MFMA operand read hits 16
-// distinct 16-byte bank groups; packed weight tiles keep their lane order.
+// grid, wave tile BM/2 tokens x 64 rows. Per 128-K step the activation tile,
+// the weight tiles and each wave's FP16 scales reach LDS through direct
+// global->LDS loads (no staging registers, no LDS store instructions) into a
+// ring of NST stages: the loads of step k+NST-1 are issued right after the
+// barrier that opens step k, and step k waits only for its own stage (every
+// wave issues the same number of loads per stage, so one vmcnt covers it).
+// Two stages keep three work-groups per CU, which measured faster than a
+// deeper ring at two.
+// Activation rows are XOR-swizzled on the load side so a 16-lane quarter of
+// an MFMA operand read hits 16 distinct 16-byte bank groups; packed weight
+// tiles keep their lane order.
 //
 // Per row-block the wave unpacks one weight tile to 16*q int8, runs the
 // MFMAs of its token blocks and folds each unit's int32 result into the FP32
@@ -33,14 +38,15 @@ __device__ __forceinline__ int a_granule(int t, int c16) {
     return (t >> 1) * 16 + (((t & 1) << 3) | (c16 ^ ((t >> 1) & 7)));
 }
 
-template <int WM, int UNIT>
+template <int WM, int UNIT, int NST>
 __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
     constexpr int BM = 2 * 16 * WM;
     constexpr int UPS = kTileK / UNIT;
     constexpr int A_BYTES = BM * kTileK;
     constexpr int B_BYTES = 8 * kTileBytes;
-    constexpr int STAGE = A_BYTES + B_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+    constexpr int S_BYTES = 4 * 4 * UPS * 32;    // per wave: 4 row-groups x UPS units x 16 FP16
+    constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     // ---- block -> (token tile, weight, n-tile), XCD-aware raster ----
     const int nblk = gridDim.x, id = blockIdx.x;
@@ -86,6 +92,12 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
         const int rg = min(rg0 + wave + 4 * i, RG - 1);       // row-groups past M: never stored
         boffs[i] = (uint32_t)rg * NT * kTileBytes + lane * 16;
     }
+    // scales: lane l < 8*UPS of each wave fetches 16 bytes (half of one
+    // row-group's 16 scales for one unit) of its 4 row-groups; LDS holds them
+    // as [j][u][16] FP16 per wave
+    const int sj = (lane >> 1) / UPS, su = (lane >> 1) % UPS;
+    const uint32_t soff =
+        ((uint32_t)min(rg0 + wn * 4 + min(sj, 3), RG - 1) * G + su) * 16 + (lane & 1) * 8;
     // (the DMA builtin takes a generic void pointer: with a typed pointer the
     // host compilation pass drops the kernel without a diagnostic)
     auto issue = [&](int kb, int st) {
@@ -94,11 +106,16 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
         const uint8_t *wk = W.codes + (size_t)kb * kTileBytes;
 #pragma unroll
         for (int i = 0; i < BM / 32; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(qk + aoffs[i]), KXW4_LDS(base + (wave + 4 * i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(qk + aoffs[i]),
+                                             KXW4_LDS(base + (wave + 4 * i) * 1024), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(wk + boffs[i]), KXW4_LDS(base + A_BYTES + (wave + 4 * i) * 1024),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(wk + boffs[i]),
+                                             KXW4_LDS(base + A_BYTES + (wave + 4 * i) * 1024), 16, 0, 0);
+        // lanes past 8*UPS are masked off; the load still counts once in vmcnt
+        if (lane < 8 * UPS)
+            __builtin_amdgcn_global_load_lds((const void *)(W.scales + (size_t)kb * UPS * 16 + soff),
+                                             KXW4_LDS(base + A_BYTES + B_BYTES + wave * (S_BYTES / 4)), 16, 0, 0);
     };
 
     // ---- per-lane read offsets ----
@@ -109,12 +126,6 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
     for (int c = 0; c < 2; ++c)
         aoff[c] = (((tw >> 1) + (n >> 1)) * 16 + (((n & 1) << 3) | ((c * 4 + g4) ^ h))) * 16;
     const int boff = A_BYTES + wn * 4 * kTileBytes + lane * 16;
-    uint32_t soffs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int rg = min(rg0 + wn * 4 + j, RG - 1);
-        soffs[j] = (uint32_t)rg * G * 16 + n;
-    }
 
     float f[WM][4][4];
 #pragma unroll
@@ -124,26 +135,25 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) f[i][j][r] = 0.0f;
 
-    uint32_t raw[UPS][4], rnx[UPS][4];         // 32-bit holders: no packing, no early wait
-    auto load_scales = [&](int kb, uint32_t (&dst)[UPS][4]) {
-#pragma unroll
-        for (int u = 0; u < UPS; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[u][j] = (W.scales + (size_t)(kb * UPS + u) * 16)[soffs[j]];
-    };
+    const int soff_lds = A_BYTES + B_BYTES + wave * (S_BYTES / 4) + n * 2;
 
+    // Ring of NST stages. Stage k % NST is issued at the top of step
+    // k - (NST - 1). At the top of step k this wave's loads of steps k ..
+    // k + NST - 2 may be outstanding (7 per stage): with three stages vmcnt(7)
+    // retires step k's, with two (or at the last step) vmcnt(0). The barrier
+    // then makes every wave's loads visible and guarantees that stage
+    // (k - 1) % NST, refilled next, is no longer read.
+    static_assert(NST == 2 || NST == 3, "two or three stages");
+    constexpr int kLoadsPerStage = BM / 32 + 2 + 1;
+    static_assert(kLoadsPerStage == 7, "vmcnt below assumes seven loads per stage");
     issue(0, 0);
-    load_scales(0, raw);
+    if (NST == 3 && NT > 1) issue(1, 1);
+    int st = 0;
     for (int kb = 0; kb < NT; ++kb) {
-        const int st = kb & 1;
-        // this wave's loads of stage st (and its scales) are done; after the
-        // barrier every wave's are, and stage st^1 is no longer read
-        __builtin_amdgcn_s_waitcnt(0x0F70);                    // vmcnt(0)
+        if (NST == 3 && kb + 1 < NT) __builtin_amdgcn_s_waitcnt(0x0F70 | 7);   // vmcnt(7)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt(0)
         lds_sync_after_dma();
-        if (kb + 1 < NT) {
-            issue(kb + 1, st ^ 1);
-            load_scales(kb + 1, rnx);
-        }
+        if (kb + NST - 1 < NT) issue(kb + NST - 1, st == 0 ? NST - 1 : st - 1);
         const uint8_t *sb = smem + st * STAGE;
         v4i A[WM][2];
 #pragma unroll
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
             const v4i zero = {0, 0, 0, 0};
             if constexpr (UNIT == 128) {
                 const v4i b0 = unpack_k64(wd.x, wd.y), b1 = unpack_k64(wd.z, wd.w);
-                const float w = half_bits_to_float(raw[0][j]);
+                const float w = half_bits_to_float(*reinterpret_cast<const uint16_t *>(sb + soff_lds + j * UPS * 32));
 #pragma unroll
                 for (int i = 0; i < WM; ++i) {
                     v4i acc = mfma_k64(A[i][0], b0, zero);
@@ -170,7 +180,8 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const v4i b = u == 0 ? unpack_k64(wd.x, wd.y) : unpack_k64(wd.z, wd.w);
-                    const float w = half_bits_to_float(raw[u][j]);
+                    const float w = half_bits_to_float(
+                        *reinterpret_cast<const uint16_t *>(sb + soff_lds + (j * UPS + u) * 32));
 #pragma unroll
                     for (int i = 0; i < WM; ++i) {
                         const v4i acc = mfma_k64(A[i][u], b, zero);
@@ -181,10 +192,7 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_kernel(const GemmArgs a) {
                 }
             }
         }
-#pragma unroll
-        for (int u = 0; u < UPS; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) raw[u][j] = rnx[u][j];
+        st = st == NST - 1 ? 0 : st + 1;
     }
 
     // ---- output ----
@@ -225,8 +233,11 @@ int launch_gemm2(GemmArgs &a, hipStream_t st) {
     a.n_tiles = nt;
     a.t_tiles = (a.T + BM - 1) / BM;
     const dim3 grid(a.n_tiles * a.t_tiles), block(kG2Threads);
-    if (a.group == 128) hipLaunchKernelGGL((gemm2_kernel<WM, 128>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((gemm2_kernel<WM, 64>), grid, block, 0, st, a);
+    constexpr int NST = 2;
+    const int ups = kTileK / a.group;
+    const size_t lds = NST * ((size_t)BM * kTileK + 8 * kTileBytes + 4 * 4 * ups * 32);
+    if (a.group == 128) hipLaunchKernelGGL((gemm2_kernel<WM, 128, NST>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((gemm2_kernel<WM, 64, NST>), grid, block, lds, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
