@@ -316,11 +316,19 @@ static int launch_dc_unit(const DecodeArgs &a, int unit, int mode, bool debug, d
 }
 
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
-    // Up to 16 tokens with one split plan per weight go to the row-wave
-    // kernel. KXW4_DECODE_KERNEL=kparallel keeps them here (used by the tests
-    // to cover this kernel at small T).
+    // Up to 16 tokens go to the row-wave kernel, the rest stay here.
+    // KXW4_DECODE_KERNEL=stream tries the persistent stream kernel first (up
+    // to 8 tokens with one split plan per weight); =kparallel skips the
+    // row-wave kernel (used by the tests to cover every kernel at the decode
+    // shapes).
     const char *force = getenv("KXW4_DECODE_KERNEL");
-    if (!debug && !(force && strcmp(force, "kparallel") == 0)) {
+    const bool use_stream = force && strcmp(force, "stream") == 0;
+    const bool no_rowwave = force && strcmp(force, "kparallel") == 0;
+    if (!debug && use_stream) {
+        const int r = launch_stream(a, st);
+        if (r != 1) return r;
+    }
+    if (!debug && !no_rowwave) {
         const int r = launch_rowwave(a, st);
         if (r != 1) return r;
     }

@@ -19,6 +19,7 @@ struct DecodeWeight {
     int seg_split[kMaxSegments];      // split count per packed segment
     int wg_begin;                     // row-wave kernel: first work-group of this weight
     int wrg;                          // row-wave kernel: waves per row-group
+    int cbeg;                         // stream kernel: first chain of this weight
 };
 
 struct DecodeArgs {
@@ -35,6 +36,7 @@ struct DecodeArgs {
     int ts;                           // tokens per work-group slice (set by the launcher)
     int smax;                         // largest split count of any token (set by the launcher)
     int total_rg;                     // row-groups over all weights (set by the launcher)
+    int total_chains;                 // stream kernel: (row-group, split) chains of all weights
 };
 
 struct GemmWeight {
@@ -77,8 +79,9 @@ int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, 
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
-// Returns 1 (nothing launched) when the shape is outside the row-wave kernel's range.
+// Return 1 (nothing launched) when the shape is outside the kernel's range.
 int launch_rowwave(DecodeArgs &a, hipStream_t st);
+int launch_stream(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
 int launch_gemm2(GemmArgs &a, hipStream_t st);

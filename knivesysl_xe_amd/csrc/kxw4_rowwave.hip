@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     // 16 zero words: the scale (and activation scale) read of a padded
     // position, so its chain step fma(p, 0, acc) leaves acc unchanged
     // (p is a finite integer and a chain that starts at +0 never holds -0)
-    float *Zero = Part + (S > 1 ? R * S * 256 : 0);
+    float *Zero = Part + (S > 1 ? R * (S - 1) * 256 : 0);
 
     // ---- stage activations and scales with direct global->LDS loads ----
     // LDS chunk x (16 bytes) is chunk x % (kc+1) of activation row x / (kc+1)
@@ -223,7 +223,8 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float v = ALT2 ? f0[r] + f1[r] : f0[r];
-                if (S > 1) Part[((rgl * S + s) * 4 + r) * 64 + lane] = v;
+                // split 0 stays in the registers of the wave that adds the splits
+                if (S > 1 && s > 0) Part[((rgl * (S - 1) + s - 1) * 4 + r) * 64 + lane] = v;
                 else res[r] = v;
             }
         }
@@ -235,8 +236,8 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
         if (!active || wj != 0) return;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float sum = 0.0f;
-            for (int s = 0; s < S; ++s) sum = sum + Part[((rgl * S + s) * 4 + r) * 64 + lane];
+            float sum = 0.0f + res[r];
+            for (int s = 1; s < S; ++s) sum = sum + Part[((rgl * (S - 1) + s - 1) * 4 + r) * 64 + lane];
             res[r] = sum;
         }
     } else if (!active) {
@@ -304,7 +305,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         w.wg_begin = wg;
         wg += (w.M / 16 + R - 1) / R;
         rmax = std::max(rmax, R);
-        if (S > 1) part = std::max(part, R * S);
+        if (S > 1) part = std::max(part, R * (S - 1));
         tiles = std::max(tiles, (a.K / kTileK + S - 1) / S);
     }
     const size_t act = (size_t)a.T * (a.K + 16);

@@ -306,9 +306,70 @@ def kparallel(monkeypatch):
     monkeypatch.setenv("KXW4_DECODE_KERNEL", "kparallel")
 
 
+@pytest.fixture
+def stream(monkeypatch):
+    # the persistent stream kernel runs only when asked for
+    monkeypatch.setenv("KXW4_DECODE_KERNEL", "stream")
+
+
 @pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
 def test_baseline_config_kparallel(name, kparallel):
     run_config(name)
+
+
+@pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
+def test_baseline_config_stream(name, stream):
+    run_config(name)
+
+
+@pytest.mark.parametrize("rows,K,T,group,block,enc,variant,forced", [
+    # fewer chains than CUs: row-groups spread over several work-groups
+    ([64], 4096, 1, 128, 0, 0, "gemv", 0),
+    ([16], 2048, 3, 64, 0, 0, "gemm", 16),
+    # cut row-groups at many boundaries, mixed weights in one fan-out
+    ([4096, 1024, 48, 16], 5120, 8, 128, 0, 0, "gemm", 0),
+    ([17408, 17408], 5120, 5, 128, 0, 0, "gemm", 0),
+    ([3072, 1040], 2048, 2, 64, 0, 0, "fanout", 0),
+    # K below one work-group's worth of tiles per segment, and K = 128
+    ([4096], 512, 4, 128, 0, 0, "gemv", 0),
+    ([1024], 128, 1, 128, 0, 0, "gemv", 0),
+    # reference mode (per-K32 activation scales, zero points)
+    ([2048, 512], 4096, 2, 64, 32, 1, "gemm", 0),
+    ([5120], 17408, 1, 64, 32, 1, "gemv", 0),
+    ([1024], 2048, 8, 32, 32, 1, "fanout", 0),
+])
+def test_stream_shapes(rows, K, T, group, block, enc, variant, forced, stream):
+    # the persistent stream kernel's work split: chain ranges per
+    # work-group, row-groups cut between work-groups, segments per weight
+    rng = np.random.default_rng(sum(rows) + K + T)
+    wts = [rand_weight(rng, M, K, group, enc) for M in rows]
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, rows[0])).astype(np.float32)
+    a = ops.quantize_act(dev(x), block)
+    q, s, sm = O.quantize_act(x, block)
+    ws = [weight(c, sc, group, enc) for c, sc in wts]
+    if variant == "gemv":
+        S = O.gemv_splits(rows[0] // 16)
+        for r in (None, res):
+            got = to_np(ops.gemv(ws[0], a, residual=None if r is None else dev(r)))
+            ref = O.project(*wts[0], group, enc, q, s, sm, block, O.VAR_GEMV, S, residual=r)
+            assert_parity(got, ref, f"gemv rows={rows[0]} residual={r is not None}")
+        return
+    if variant == "fanout":
+        ys = ops.gemv_fanout(ws, a)
+        S = O.gemv_splits(sum(rows) // 16)
+        refs = [O.project(c, sc, group, enc, q, s, sm, block, O.VAR_FANOUT, S) for c, sc in wts]
+    else:
+        ys = ops.gemm_fanout(ws, a, torch.float32, forced_splits=forced)
+        refs = [O.project(c, sc, group, enc, q, s, sm, block, O.VAR_GEMM,
+                          O.segment_splits(T, c.shape[0], K, None, forced)) for c, sc in wts]
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_parity(to_np(y), ref, f"{variant} weight {i} rows={rows[i]}")
+    # a second launch reuses the exchange counters the first one reset
+    ys2 = ops.gemv_fanout(ws, a) if variant == "fanout" else \
+        ops.gemm_fanout(ws, a, torch.float32, forced_splits=forced)
+    for y, y2 in zip(ys, ys2):
+        assert np.array_equal(to_np(y).view(np.uint32), to_np(y2).view(np.uint32))
 
 
 @pytest.fixture
