@@ -23,6 +23,7 @@ namespace kxw4 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kTileK = 128;        // K extent of one packed weight tile
@@ -46,6 +47,14 @@ __device__ __forceinline__ v4i unpack_k64(uint32_t d0, uint32_t d1) {
 __device__ __forceinline__ long unpack_k32(uint32_t d) {
     const uint64_t lo = nib_lo16(d), hi = nib_hi16(d);
     return (long)(lo | (hi << 32));
+}
+
+// v_mfma_i32_32x32x32_i8: lane l supplies row (A) / column (B) l%32 and the
+// 16 K slots of K group l/32 (the same slots for both operands); result
+// register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32] (checked on the
+// MI355X against a host product of random operands).
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ v4i mfma_k64(v4i a, v4i b, v4i c) {

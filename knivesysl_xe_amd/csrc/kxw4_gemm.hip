@@ -352,10 +352,17 @@ static void launch_wm_unit(const GemmArgs &a, int mode, bool splits, bool debug,
 }
 
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
-    // The per-token, one-split mode goes to the LDS-DMA kernel;
-    // KXW4_GEMM_KERNEL=general keeps it here (the tests cover both).
+    // The per-token, one-split mode goes to the large-tile kernel;
+    // KXW4_GEMM_KERNEL=gemm2 takes the smaller-tile LDS-DMA kernel, =general
+    // keeps it here (the tests cover all three).
     const char *force = getenv("KXW4_GEMM_KERNEL");
-    if (!debug && !(force && strcmp(force, "general") == 0)) {
+    const bool general = force && strcmp(force, "general") == 0;
+    const bool g2 = force && strcmp(force, "gemm2") == 0;
+    if (!debug && !general && !g2) {
+        const int r = launch_gemm3(a, st);
+        if (r != 1) return r;
+    }
+    if (!debug && !general) {
         const int r = launch_gemm2(a, st);
         if (r != 1) return r;
     }

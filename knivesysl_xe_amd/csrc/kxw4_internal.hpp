@@ -78,6 +78,9 @@ int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T,
 int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 
+// compute units of the current device (cached per device)
+int device_cus();
+
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
 // Return 1 (nothing launched) when the shape is outside the kernel's range.
 int launch_rowwave(DecodeArgs &a, hipStream_t st);
@@ -85,5 +88,6 @@ int launch_stream(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
 int launch_gemm2(GemmArgs &a, hipStream_t st);
+int launch_gemm3(GemmArgs &a, hipStream_t st);
 
 }  // namespace kxw4

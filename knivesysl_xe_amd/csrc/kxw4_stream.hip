@@ -522,7 +522,7 @@ static int st_tp(const DecodeArgs &a, int tp, int grid, size_t lds, hipStream_t 
     }
 }
 
-static int device_cus() {
+int device_cus() {
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kStMaxWg;

@@ -374,9 +374,55 @@ def test_stream_shapes(rows, K, T, group, block, enc, variant, forced, stream):
 
 @pytest.fixture
 def gemm_general(monkeypatch):
-    # the per-token prefill shapes normally run on the LDS-DMA GEMM kernel;
-    # this keeps the general GEMM kernel covered on them
+    # the per-token prefill shapes normally run on the large-tile GEMM
+    # kernel; this keeps the general GEMM kernel covered on them
     monkeypatch.setenv("KXW4_GEMM_KERNEL", "general")
+
+
+@pytest.fixture
+def gemm2(monkeypatch):
+    # and this the smaller-tile LDS-DMA kernel
+    monkeypatch.setenv("KXW4_GEMM_KERNEL", "gemm2")
+
+
+@pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
+def test_baseline_config_gemm2(name, gemm2):
+    run_config(name)
+
+
+def test_baseline_cfg4_rows_gemm2(gemm2):
+    run_config("cfg4", rows=[(0, 256), (17152, 17408)])
+
+
+@pytest.fixture(params=["0", "1", "2", "3", "4"])
+def gemm3_tile(request, monkeypatch):
+    # every tile configuration of the large-tile kernel
+    monkeypatch.setenv("KXW4_GEMM3_TILE", request.param)
+
+
+@pytest.mark.parametrize("rows,K,T,group", [
+    # partial token and row tiles, fan-out weights of different heights,
+    # fewer K steps than ring stages, both group sizes
+    ([1040], 1024, 300, 128), ([1040, 2064], 640, 257, 64), ([4096], 128, 520, 128),
+    ([256], 5120, 2048, 64)])
+def test_gemm3_shapes(rows, K, T, group, gemm3_tile):
+    rng = np.random.default_rng(sum(rows) + K + T)
+    wts = [rand_weight(rng, M, K, group, 0) for M in rows]
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, rows[0])).astype(np.float32)
+    a = ops.quantize_act(dev(x), 0)
+    q, s, sm = O.quantize_act(x, 0)
+    ws = [weight(c, sc, group, 0) for c, sc in wts]
+    sps = [O.segment_splits(T, M, K) for M in rows]
+    # one split per token: the shapes the large-tile kernel takes
+    assert all(np.all(sp == 1) for sp in sps)
+    ys = ops.gemm_fanout(ws, a, torch.float32)
+    for i, ((c, sc), y, sp) in enumerate(zip(wts, ys, sps)):
+        ref = O.project(c, sc, group, 0, q, s, sm, 0, O.VAR_GEMM, sp)
+        assert_parity(to_np(y), ref, f"weight {i} rows={rows[i]}")
+    got = to_np(ops.gemm(ws[0], a, torch.bfloat16, residual=dev(res)))
+    ref = O.project(*wts[0], group, 0, q, s, sm, 0, O.VAR_GEMM, sps[0], residual=res, out_bf16=True)
+    assert_parity(got, ref, "bf16 + residual", bf16=True)
 
 
 @pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
