@@ -315,17 +315,28 @@ static int launch_dc_unit(const DecodeArgs &a, int unit, int mode, bool debug, d
     return launch_dc<AT, 32>(a, mode, debug, grid, lds, st);
 }
 
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
     // Up to 16 tokens go to the row-wave kernel, the rest stay here.
-    // KXW4_DECODE_KERNEL=stream tries the persistent stream kernel first (up
-    // to 8 tokens with one split plan per weight); =kparallel skips the
-    // row-wave kernel (used by the tests to cover every kernel at the decode
-    // shapes).
+    // KXW4_DECODE_KERNEL=persist tries the persistent kernel first (up to 8
+    // tokens with one split plan per weight); =kparallel skips the row-wave
+    // kernel (used by the tests to cover every kernel at the decode shapes).
     const char *force = getenv("KXW4_DECODE_KERNEL");
-    const bool use_stream = force && strcmp(force, "stream") == 0;
+    const bool use_persist = force && strcmp(force, "persist") == 0;
     const bool no_rowwave = force && strcmp(force, "kparallel") == 0;
-    if (!debug && use_stream) {
-        const int r = launch_stream(a, st);
+    if (!debug && use_persist) {
+        const int r = launch_persist(a, st);
         if (r != 1) return r;
     }
     if (!debug && !no_rowwave) {

@@ -19,7 +19,7 @@ struct DecodeWeight {
     int seg_split[kMaxSegments];      // split count per packed segment
     int wg_begin;                     // row-wave kernel: first work-group of this weight
     int wrg;                          // row-wave kernel: waves per row-group
-    int cbeg;                         // stream kernel: first chain of this weight
+    int cbeg;                         // persistent kernel: first chain of this weight
 };
 
 struct DecodeArgs {
@@ -36,7 +36,9 @@ struct DecodeArgs {
     int ts;                           // tokens per work-group slice (set by the launcher)
     int smax;                         // largest split count of any token (set by the launcher)
     int total_rg;                     // row-groups over all weights (set by the launcher)
-    int total_chains;                 // stream kernel: (row-group, split) chains of all weights
+    int total_chains;                 // persistent kernel: (row-group, split) chains of all weights
+    int ps_smin, ps_nrg, ps_rslots, ps_cmax;   // persistent kernel LDS layout (set by the launcher)
+    int ps_q, ps_r;                   // persistent kernel: chains = ps_q * grid + ps_r
 };
 
 struct GemmWeight {
@@ -84,7 +86,7 @@ int device_cus();
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
 // Return 1 (nothing launched) when the shape is outside the kernel's range.
 int launch_rowwave(DecodeArgs &a, hipStream_t st);
-int launch_stream(DecodeArgs &a, hipStream_t st);
+int launch_persist(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
 int launch_gemm2(GemmArgs &a, hipStream_t st);

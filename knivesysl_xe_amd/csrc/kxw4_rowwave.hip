@@ -88,7 +88,10 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
 
     // ---- the wave's first split and its ring ----
     const int sb = wj * S / wrg, se = (wj + 1) * S / wrg;
-    int u0 = (int)((long long)Nu * sb / S), u1 = (int)((long long)Nu * (sb + 1) / S);
+    // split ranges [Nu*s/S, Nu*(s+1)/S); S is a power of two (checked by
+    // the launcher) and Nu*S fits in 32 bits
+    const int ls = __builtin_ctz(S);
+    int u0 = (Nu * sb) >> ls, u1 = (Nu * (sb + 1)) >> ls;
     int kt0 = u0 / UPS, ntw = (u1 + UPS - 1) / UPS - kt0;
     const v4u *wrow = reinterpret_cast<const v4u *>(W.codes + (size_t)rg * NT * kTileBytes) + lane;
     v4u ring[PF];
@@ -129,8 +132,8 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     if (active) {
         for (int s = sb; s < se; ++s) {
             if (s != sb) {
-                u0 = (int)((long long)Nu * s / S);
-                u1 = (int)((long long)Nu * (s + 1) / S);
+                u0 = (Nu * s) >> ls;
+                u1 = (Nu * (s + 1)) >> ls;
                 kt0 = u0 / UPS;
                 ntw = (u1 + UPS - 1) / UPS - kt0;
 #pragma unroll
@@ -299,7 +302,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         const int S = w.seg_split[0];
         for (int s = 1; s < a.seg_count; ++s)
             if (w.seg_split[s] != S) return 1;
-        if (S < 1 || S > 16) return 1;
+        if (S < 1 || S > 16 || (S & (S - 1))) return 1;
         w.wrg = std::min(S, kRwWaves);
         const int R = kRwWaves / w.wrg;
         w.wg_begin = wg;

@@ -307,9 +307,9 @@ def kparallel(monkeypatch):
 
 
 @pytest.fixture
-def stream(monkeypatch):
-    # the persistent stream kernel runs only when asked for
-    monkeypatch.setenv("KXW4_DECODE_KERNEL", "stream")
+def persist(monkeypatch):
+    # the persistent decode kernel runs only when asked for
+    monkeypatch.setenv("KXW4_DECODE_KERNEL", "persist")
 
 
 @pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
@@ -318,7 +318,7 @@ def test_baseline_config_kparallel(name, kparallel):
 
 
 @pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
-def test_baseline_config_stream(name, stream):
+def test_baseline_config_persist(name, persist):
     run_config(name)
 
 
@@ -338,9 +338,9 @@ def test_baseline_config_stream(name, stream):
     ([5120], 17408, 1, 64, 32, 1, "gemv", 0),
     ([1024], 2048, 8, 32, 32, 1, "fanout", 0),
 ])
-def test_stream_shapes(rows, K, T, group, block, enc, variant, forced, stream):
-    # the persistent stream kernel's work split: chain ranges per
-    # work-group, row-groups cut between work-groups, segments per weight
+def test_persist_shapes(rows, K, T, group, block, enc, variant, forced, persist):
+    # the persistent kernel's work split: chain ranges per work-group,
+    # row-groups cut between work-groups, whole and K-split chains
     rng = np.random.default_rng(sum(rows) + K + T)
     wts = [rand_weight(rng, M, K, group, enc) for M in rows]
     x = rng.standard_normal((T, K)).astype(np.float32)
