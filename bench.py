@@ -157,16 +157,12 @@ def measure(cfg, steps, warmup, eager=False):
     run(copies[0])
     torch.cuda.synchronize()
     exact = check_against_oracle(cfg, inp, outs)
-    # activation quantization, timed on its own for reference
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # activation quantization, timed on its own for reference (graph replay
+    # of launches into one reused output, like the projection)
     from knivesysl_xe_amd import ops
-    ops.quantize_act(x, 0)
-    e0.record()
-    for _ in range(20):
-        ops.quantize_act(x, 0)
-    e1.record()
-    torch.cuda.synchronize()
-    quant_us = e0.elapsed_time(e1) / 20 * 1e3
+    qa = ops.QuantAct.empty(cfg.tokens, cfg.K, 0)
+    qsecs, _ = time_graph(lambda _c: ops.quantize_act(x, 0, out=qa), [None], 20, 2)
+    quant_us = qsecs / 20 * 1e6
     per = secs / steps
     res = {
         "kernel_us": per * 1e6,

@@ -134,8 +134,90 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
     }
 }
 
+// Per-token mode with plain loads, one pass: each thread holds chunks of 8
+// consecutive elements (16-byte bf16 / 32-byte f32 loads) in registers for the
+// whole row, so the row is read once. The MFMA slot order keeps the 8 codes of
+// a chunk contiguous: chunk c of 64-element chunk h lands at byte
+// 64h + 16(c & 3) + 8((c >> 2) & 1), one 8-byte store. The four chunks of a
+// K32 block sit in four consecutive lanes, so their code sum is a 4-lane
+// shuffle.
+template <int P, int NCH>
+__global__ __launch_bounds__(kQThreads) void quantize_tok_kernel(QuantArgs a) {
+    static_assert(P == kLoadF32 || P == kLoadBF16, "plain loads");
+    __shared__ float red[kQThreads / 64];
+    const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
+    const int nch = K / 8;
+    float v[NCH][8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = tid + c * kQThreads;
+        if (idx < nch) {
+            if constexpr (P == kLoadBF16) {
+                const uint4 x = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + (size_t)t * K)[idx];
+                const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[c][2 * j] = __uint_as_float(w[j] << 16);
+                    v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+                }
+            } else {
+                const float4 *row = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + (size_t)t * K);
+                const float4 x0 = row[2 * idx], x1 = row[2 * idx + 1];
+                v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
+                v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+        }
+    }
+    mx = block_reduce_max(mx, red);
+    const float s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+    if (tid == 0) a.scale[t] = s;
+    int8_t *qrow = a.q + (size_t)t * K;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = tid + c * kQThreads;
+        // whole K32 blocks (4 chunks) per 4-lane group: nch % 4 == 0
+        if (idx - (tid & 3) < nch) {
+            uint32_t lo = 0, hi = 0;
+            int sum = 0;
+            if (idx < nch) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int8_t q = quantize_one(v[c][j], s);
+                    sum += q;
+                    if (j < 4) lo |= (uint32_t)(uint8_t)q << (8 * j);
+                    else hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
+                }
+                *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
+                    make_uint2(lo, hi);
+            }
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            if (a.sum && (idx & 3) == 0 && idx < nch) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
+        }
+    }
+}
+
 template <int P>
 static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
+    if constexpr (P == kLoadF32 || P == kLoadBF16) {
+        // one pass with the row in registers, up to 20480 elements
+        const int nch = a.K / 8;
+        if (block != 32 && a.K % 32 == 0) {
+            if (nch <= 2 * kQThreads)
+                hipLaunchKernelGGL((quantize_tok_kernel<P, 2>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            else if (nch <= 4 * kQThreads)
+                hipLaunchKernelGGL((quantize_tok_kernel<P, 4>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            else if (nch <= 10 * kQThreads)
+                hipLaunchKernelGGL((quantize_tok_kernel<P, 10>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            else
+                goto general;
+            return hipGetLastError() == hipSuccess ? 0 : -6;
+        }
+    }
+general:
     if (block == 32)
         hipLaunchKernelGGL((quantize_kernel<P, false>), dim3(a.T), dim3(kQThreads), 0, st, a);
     else

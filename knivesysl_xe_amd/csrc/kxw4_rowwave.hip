@@ -267,8 +267,7 @@ static int rw_launch(const DecodeArgs &a, dim3 grid, size_t lds, hipStream_t st)
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
-// pf8: the longest split streams enough tiles for a deeper ring (plain
-// per-token mode only; the general mode keeps 4)
+// pf8: a deeper ring (plain per-token mode only; the general mode keeps 4)
 template <int TT, int UNIT>
 static int rw_mode(const DecodeArgs &a, int mode, bool pf8, dim3 grid, size_t lds, hipStream_t st) {
     const bool alt2 = a.variant == kVarGemv;
@@ -316,7 +315,10 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     const size_t lds = act + scales + (mode != 0 ? (size_t)2 * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
     if (lds > kRwLdsMax) return 1;
     const dim3 grid(wg);
-    const bool pf8 = tiles >= 16;
+    // KXW4_ROWWAVE_PF=8 takes the deeper ring (measured slower: more loads in
+    // flight at the start delay the staging)
+    const char *pfe = getenv("KXW4_ROWWAVE_PF");
+    const bool pf8 = pfe && atoi(pfe) == 8 && tiles >= 16;
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, lds, st);
     return rw_unit<16>(a, unit, mode, pf8, grid, lds, st);
 }

@@ -160,9 +160,13 @@ def act_codes_natural(a: QuantAct) -> torch.Tensor:
     return a.q[:, perm]
 
 
-def quantize_act(x: torch.Tensor, block: int = 0) -> QuantAct:
+def quantize_act(x: torch.Tensor, block: int = 0, out: Optional[QuantAct] = None) -> QuantAct:
+    """Quantize [T][K] f32/bf16 activations; `out` (same T, K, block) is
+    reused when given, so the call allocates nothing."""
     T, K = x.shape
-    a = QuantAct.empty(T, K, block, x.device)
+    if out is not None and (out.T, out.K, out.block) != (T, K, block):
+        raise ValueError("out does not match the activation shape / block")
+    a = out if out is not None else QuantAct.empty(T, K, block, x.device)
     check("kxw4_quantize_act", lib().kxw4_quantize_act(
         _ptr(x), _dtype_code(x.dtype), T, K, block, _ptr(a.q), _ptr(a.scale), _ptr(a.sum),
         _stream()))
