@@ -19,6 +19,7 @@ struct DecodeWeight {
     int seg_split[kMaxSegments];      // split count per packed segment
     int wg_begin;                     // row-wave kernel: first work-group of this weight
     int wrg;                          // row-wave kernel: waves per row-group
+    int wg_count;                     // row-wave kernel: work-groups of this weight
     int cbeg;                         // persistent kernel: first chain of this weight
 };
 

@@ -27,12 +27,12 @@
 
 namespace kxw4 {
 
-constexpr int kRwWaves = 8;
-constexpr int kRwThreads = 64 * kRwWaves;
-constexpr size_t kRwLdsMax = 64 * 1024;
+constexpr int kRwWaves = 8;                 // waves per work-group by default
+constexpr int kRwMaxWaves = 16;
+constexpr size_t kRwLdsMax = 160 * 1024;
 
 template <int TT, int UNIT, int MODE, bool ALT2, int PF>
-__global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeArgs a) {
     constexpr int UPS = kTileK / UNIT;
     static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -41,7 +41,12 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     for (int i = 1; i < a.count; ++i)
         if ((int)blockIdx.x >= a.w[i].wg_begin) wi = i;
     const DecodeWeight &W = a.w[wi];
-    const int S = W.seg_split[0], wrg = W.wrg, R = kRwWaves / wrg;
+    // the work-group's waves: rows of wrg waves, one per row-group; R is the
+    // most row-groups a work-group of this weight owns (the LDS sizes
+    // follow it)
+    const int nthreads = blockDim.x;
+    const int S = W.seg_split[0], wrg = W.wrg;
+    const int R = (W.M / 16 + W.wg_count - 1) / W.wg_count;
     const int K = a.K, T = a.T, M = W.M;
     const int NT = K / kTileK, Nu = K / UNIT, G = K / a.group;
     const int gsh = __builtin_ctz(a.group / UNIT);
@@ -49,8 +54,11 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, n = lane & 15, g4 = lane >> 4;
     const int rgl = wave / wrg, wj = wave - rgl * wrg;
-    const int rg0 = ((int)blockIdx.x - W.wg_begin) * R;      // first row-group of the work-group
-    const int nrg = min(R, M / 16 - rg0);                     // row-groups it owns
+    // row-groups [rg0, rg0 + nrg) of the weight: the weight's wg_count
+    // work-groups split its row-groups as evenly as possible
+    const int bl = (int)blockIdx.x - W.wg_begin, RGw = M / 16;
+    const int rg0 = bl * RGw / W.wg_count;
+    const int nrg = (bl + 1) * RGw / W.wg_count - rg0;
     const bool active = rgl < nrg;
     const int rg = rg0 + (active ? rgl : 0);
 
@@ -71,7 +79,7 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     const int kc = K / 16;
     const int act_chunks = T * (kc + 1);
     const int total = act_chunks + nrg * G * 2;
-    for (int c0 = wave * 64; c0 < total; c0 += kRwThreads) {
+    for (int c0 = wave * 64; c0 < total; c0 += nthreads) {
         const int x = c0 + lane;
         if (x < total) {
             const void *src;
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
     const bool ref_block = a.block == 32, zp = a.scale_enc == 1;
     if (MODE != 0) {
         // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
-        for (int x = tid; x < Nu * 16; x += kRwThreads) {
+        for (int x = tid; x < Nu * 16; x += nthreads) {
             const int u = x >> 4, t = min(x & 15, T - 1);
             Asc[x] = ref_block ? a.ascale[(size_t)t * (K / 32) + u] : 1.0f;
             int sm = 0;
@@ -262,32 +270,40 @@ __global__ __launch_bounds__(kRwThreads, 3) void rowwave_kernel(const DecodeArgs
 }
 
 template <int TT, int UNIT, int MODE, bool ALT2, int PF>
-static int rw_launch(const DecodeArgs &a, dim3 grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((rowwave_kernel<TT, UNIT, MODE, ALT2, PF>), grid, dim3(kRwThreads), lds, st, a);
+static int rw_launch(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+    auto k = rowwave_kernel<TT, UNIT, MODE, ALT2, PF>;
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kRwLdsMax) != hipSuccess)
+            return -6;
+        attr = true;
+    }
+    hipLaunchKernelGGL(k, grid, block, lds, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
 // pf8: a deeper ring (plain per-token mode only; the general mode keeps 4)
 template <int TT, int UNIT>
-static int rw_mode(const DecodeArgs &a, int mode, bool pf8, dim3 grid, size_t lds, hipStream_t st) {
+static int rw_mode(const DecodeArgs &a, int mode, bool pf8, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
     const bool alt2 = a.variant == kVarGemv;
     if (mode == 0) {
         if (pf8)
-            return alt2 ? rw_launch<TT, UNIT, 0, true, 8>(a, grid, lds, st)
-                        : rw_launch<TT, UNIT, 0, false, 8>(a, grid, lds, st);
-        return alt2 ? rw_launch<TT, UNIT, 0, true, 4>(a, grid, lds, st)
-                    : rw_launch<TT, UNIT, 0, false, 4>(a, grid, lds, st);
+            return alt2 ? rw_launch<TT, UNIT, 0, true, 8>(a, grid, block, lds, st)
+                        : rw_launch<TT, UNIT, 0, false, 8>(a, grid, block, lds, st);
+        return alt2 ? rw_launch<TT, UNIT, 0, true, 4>(a, grid, block, lds, st)
+                    : rw_launch<TT, UNIT, 0, false, 4>(a, grid, block, lds, st);
     }
-    return alt2 ? rw_launch<TT, UNIT, 1, true, 4>(a, grid, lds, st)
-                : rw_launch<TT, UNIT, 1, false, 4>(a, grid, lds, st);
+    return alt2 ? rw_launch<TT, UNIT, 1, true, 4>(a, grid, block, lds, st)
+                : rw_launch<TT, UNIT, 1, false, 4>(a, grid, block, lds, st);
 }
 
 template <int TT>
-static int rw_unit(const DecodeArgs &a, int unit, int mode, bool pf8, dim3 grid, size_t lds,
+static int rw_unit(const DecodeArgs &a, int unit, int mode, bool pf8, dim3 grid, dim3 block, size_t lds,
                    hipStream_t st) {
-    if (unit == 128) return rw_mode<TT, 128>(a, mode, pf8, grid, lds, st);
-    if (unit == 64) return rw_mode<TT, 64>(a, mode, pf8, grid, lds, st);
-    return rw_mode<TT, 32>(a, mode, pf8, grid, lds, st);
+    if (unit == 128) return rw_mode<TT, 128>(a, mode, pf8, grid, block, lds, st);
+    if (unit == 64) return rw_mode<TT, 64>(a, mode, pf8, grid, block, lds, st);
+    return rw_mode<TT, 32>(a, mode, pf8, grid, block, lds, st);
 }
 
 int launch_rowwave(DecodeArgs &a, hipStream_t st) {
@@ -295,7 +311,13 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     const int unit = a.block == 32 ? 32 : a.group;
     const int nu = a.K / unit, g = a.K / a.group;
     const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
-    int wg = 0, rmax = 1, part = 0, tiles = 0;
+    // Default shape: 8 waves per work-group, 8 / wrg row-groups each. When
+    // that leaves a partial last round of work-groups over the CUs (the CUs
+    // holding one more work-group finish last), the weights' row-groups are
+    // instead dealt to exactly k work-groups per CU, each owning
+    // ceil(row-groups / work-groups) row-groups at most, and the LDS request
+    // keeps a (k+1)-th work-group off every CU.
+    int rg_total = 0, wrg_max = 1, tiles = 0;
     for (int i = 0; i < a.count; ++i) {
         DecodeWeight &w = a.w[i];
         const int S = w.seg_split[0];
@@ -303,24 +325,58 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
             if (w.seg_split[s] != S) return 1;
         if (S < 1 || S > 16 || (S & (S - 1))) return 1;
         w.wrg = std::min(S, kRwWaves);
-        const int R = kRwWaves / w.wrg;
-        w.wg_begin = wg;
-        wg += (w.M / 16 + R - 1) / R;
-        rmax = std::max(rmax, R);
-        if (S > 1) part = std::max(part, R * (S - 1));
+        wrg_max = std::max(wrg_max, w.wrg);
+        rg_total += w.M / 16;
         tiles = std::max(tiles, (a.K / kTileK + S - 1) / S);
     }
+    int wg_default = 0;
+    for (int i = 0; i < a.count; ++i) wg_default += (a.w[i].M / 16 + kRwWaves / a.w[i].wrg - 1) / (kRwWaves / a.w[i].wrg);
+    const int cus = device_cus();
+    const int k = wg_default / cus;
+    bool balanced = k >= 1 && wg_default % cus != 0 && !getenv("KXW4_ROWWAVE_DEFAULT_GRID");
+    int wg = 0, waves = kRwWaves, rmax = 1, part = 0;
+    auto plan = [&](bool bal) {
+        wg = 0;
+        waves = bal ? 0 : kRwWaves;
+        rmax = 1;
+        part = 0;
+        for (int i = 0; i < a.count; ++i) {
+            DecodeWeight &w = a.w[i];
+            const int RG = w.M / 16, S = w.seg_split[0];
+            int n = bal ? (int)(((long long)k * cus * RG + rg_total / 2) / rg_total)
+                        : (RG + kRwWaves / w.wrg - 1) / (kRwWaves / w.wrg);
+            n = std::max(1, std::min(n, RG));
+            const int R = (RG + n - 1) / n;
+            w.wg_begin = wg;
+            w.wg_count = n;
+            wg += n;
+            rmax = std::max(rmax, R);
+            if (bal) waves = std::max(waves, R * w.wrg);
+            if (S > 1) part = std::max(part, R * (S - 1));
+        }
+    };
+    if (balanced) {
+        // keep the balanced plan only when it lowers the most row-groups a
+        // CU streams
+        plan(false);
+        const int load_default = (wg_default + cus - 1) / cus * rmax;
+        plan(true);
+        if (waves > kRwMaxWaves || k * rmax >= load_default) balanced = false;
+    }
+    if (!balanced) plan(false);
     const size_t act = (size_t)a.T * (a.K + 16);
     const size_t scales = (size_t)rmax * g * 32;
-    const size_t lds = act + scales + (mode != 0 ? (size_t)2 * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
+    size_t lds = act + scales + (mode != 0 ? (size_t)2 * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
     if (lds > kRwLdsMax) return 1;
+    if (balanced) lds = std::max(lds, (size_t)160 * 1024 / (k + 1) + 1024);
+    const dim3 block(64 * waves);
     const dim3 grid(wg);
     // KXW4_ROWWAVE_PF=8 takes the deeper ring (measured slower: more loads in
     // flight at the start delay the staging)
     const char *pfe = getenv("KXW4_ROWWAVE_PF");
     const bool pf8 = pfe && atoi(pfe) == 8 && tiles >= 16;
-    if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, lds, st);
-    return rw_unit<16>(a, unit, mode, pf8, grid, lds, st);
+    if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, block, lds, st);
+    return rw_unit<16>(a, unit, mode, pf8, grid, block, lds, st);
 }
 
 }  // namespace kxw4
