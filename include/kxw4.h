@@ -142,6 +142,20 @@ int kxw4_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T,
                        int H, float eps, int block, int8_t *q, float *scale,
                        int32_t *sum, void *stream);
 
+/* s4 activations of the W4A4 GEMM: x_quantize_act_chunk_s4
+ * (kernels_dpas.cpp:1492-1498 over 1149-1197). x[T][K] (KXW4_F32 or
+ * KXW4_BF16) -> per (token, K64) block s = absmax/7 (1 when the block max is
+ * not positive), codes clamp(rint(v/s), -7, 7) and their exact sum.
+ *   q4    : T*K/2 bytes, [K/128][T][64 B]: the 64 bytes of (128-K step kb,
+ *           token t) have the nibble order of a packed weight tile row —
+ *           dword i of 16-byte lane group g holds k = 128kb + 32i + 8g + b,
+ *           b = 0..3 in the low nibbles of bytes 0..3, b = 4..7 in the high
+ *           nibbles (two's complement).
+ *   scale : [K/64][T] FP32, sum: [K/64][T] int32 (the reference's layout).
+ * Requires K % 128 == 0. Buffer sizes equal the reference's (aq4, as4, asum4). */
+int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4,
+                         float *scale, int32_t *sum, void *stream);
+
 /* ---- projections -------------------------------------------------------- */
 
 /* x_gemv_w4a8_core arithmetic (kernels_dpas.cpp:586-675) with the
@@ -174,6 +188,16 @@ int kxw4_gemm(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
 int kxw4_gemm_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
                      const kxw4_act_t *a, int y_dtype, const int *offsets,
                      int segments, int forced_splits, void *stream);
+
+/* x_gemm_w4a4 (kernels_dpas.cpp:1500-1571): s4 activations from
+ * kxw4_quantize_act_s4 against a K64 weight with FP16|zp scales (group 64,
+ * KXW4_SCALE_FP16_ZP4, else -1). One serial FP32 chain per output over the
+ * K64 groups, acc += (float)(d - zp*sum) * (ws*as); y[T][M] FP32 or BF16,
+ * plus residual[T][M] (may be NULL). Any T >= 1 (the reference requires
+ * T % 8 == 0; its shim keeps that check). */
+int kxw4_gemm_w4a4(const kxw4_weight_t *w, const uint8_t *q4, const float *scale,
+                   const int32_t *sum, int T, void *y, int y_dtype,
+                   const float *residual, void *stream);
 
 /* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
  * else group), from the same unpack and MFMA code as the projections. */

@@ -10,6 +10,9 @@
 //   * activation codes written by x_quantize_act_s8 / x_quantize_act_chunk
 //     follow kxw4_act_t's slot order, and sums are per K32 block (the
 //     buffers the reference sizes K/16 or [K/32][T] are large enough);
+//   * s4 codes written by x_quantize_act_chunk_s4 follow kxw4.h's s4 tile
+//     order (T*K/2 bytes, as the reference sizes aq4); scales and sums keep
+//     the reference's [K/64][T] layout;
 //   * every call runs on the stream set by kxw4_compat_set_stream (the null
 //     stream by default), the counterpart of the reference's one in-order
 //     queue per rank (decode.cpp:86-99).
@@ -75,6 +78,13 @@ int x_gemm_w4a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as
                 const int32_t *d_asum, float *d_y, int T, const int *offsets = nullptr,
                 int segments = 0);
 int x_gemv_w4a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual = nullptr);
+// kernels_dpas.cpp:1492-1498: s4 activations of the W4A4 GEMM.
+void x_quantize_act_chunk_s4(const float *d_x, int K, int T, uint8_t *d_aq4, float *d_as4,
+                             int32_t *d_asum4);
+// kernels_dpas.cpp:1500-1571: -1 unless the weight is the K64 tier, -2 for a
+// missing operand or T % 8 != 0.
+int x_gemm_w4a4(const tq_qmma_weight_t *w, const uint8_t *d_aq4, const float *d_as4,
+                const int32_t *d_asum4, float *d_y, int T);
 // kernels_core.cpp:235-252: W4A8 when s4_ready, otherwise KXW4_ETIER.
 int x_gemv_qmma_prepared(const tq_qmma_weight_t *w, const float *d_x, float *d_y,
                          const float *d_residual = nullptr);

@@ -45,10 +45,12 @@ SIGNATURES = {
     "kxw4_quantize_act": (I, [P, I, I, I, I, P, P, P, P]),
     "kxw4_silu_mul_quant": (I, [P, P, P, I, I, I, P, P, P, P]),
     "kxw4_rmsnorm_quant": (I, [P, P, P, I, I, F, I, P, P, P, P]),
+    "kxw4_quantize_act_s4": (I, [P, I, I, I, P, P, P, P]),
     "kxw4_gemv": (I, [WP, AP, P, I, P, I, P]),
     "kxw4_gemv_fanout": (I, [C.POINTER(WP), C.POINTER(P), I, AP, I, P]),
     "kxw4_gemm": (I, [WP, AP, P, I, P, C.POINTER(I), I, I, P]),
     "kxw4_gemm_fanout": (I, [C.POINTER(WP), C.POINTER(P), I, AP, I, C.POINTER(I), I, I, P]),
+    "kxw4_gemm_w4a4": (I, [WP, P, P, P, I, P, I, P, P]),
     "kxw4_partials": (I, [WP, AP, P, P]),
 }
 

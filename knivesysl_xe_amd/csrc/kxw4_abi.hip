@@ -237,6 +237,13 @@ int kxw4_quantize_act(const void *x, int x_dtype, int T, int K, int block, int8_
     return launch_quantize(x, x_dtype, T, K, block, q, scale, sum, as_stream(stream));
 }
 
+int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4, float *scale,
+                         int32_t *sum, void *stream) {
+    if (!x || !q4 || !scale || !sum) return KXW4_EARG;
+    if (T <= 0 || K <= 0 || K % 128 || (x_dtype != KXW4_F32 && x_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    return launch_quantize_s4(x, x_dtype, T, K, q4, scale, sum, as_stream(stream));
+}
+
 int kxw4_silu_mul_quant(float *out, const float *gate, const float *up, int T, int K, int block,
                         int8_t *q, float *scale, int32_t *sum, void *stream) {
     if (!gate || !up || !q || !scale) return KXW4_EARG;
@@ -304,6 +311,33 @@ int kxw4_gemm_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
                      int forced_splits, void *stream) {
     return gemm_common(ws, ys, count, a, y_dtype, nullptr, offsets, segments, forced_splits,
                        nullptr, as_stream(stream));
+}
+
+// x_gemm_w4a4's checks (kernels_dpas.cpp:1503-1504): -1 for a weight that is
+// not the K64 tier with FP16|zp scales, -2 for missing operands or shapes.
+int kxw4_gemm_w4a4(const kxw4_weight_t *w, const uint8_t *q4, const float *scale, const int32_t *sum,
+                   int T, void *y, int y_dtype, const float *residual, void *stream) {
+    if (!w || !w->codes || !w->scales || w->group != 64 || w->scale_enc != KXW4_SCALE_FP16_ZP4)
+        return KXW4_EARG;
+    if (!valid_shape(w->M, w->K, w->group)) return KXW4_ESHAPE;
+    if (!q4 || !scale || !sum || !y || T <= 0) return KXW4_ESHAPE;
+    if (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16) return KXW4_ESHAPE;
+    // 32-bit per-lane offsets inside the kernel
+    if ((long long)T * 64 >= (1ll << 31) || (long long)w->M * w->K / 2 >= (1ll << 31) ||
+        (long long)(w->K / 64) * T >= (1ll << 31))
+        return KXW4_ESHAPE;
+    W4a4Args args{};
+    args.q4 = q4;
+    args.as4 = scale;
+    args.codes = w->codes;
+    args.scales = w->scales;
+    args.y = y;
+    args.residual = residual;
+    args.M = w->M;
+    args.K = w->K;
+    args.T = T;
+    args.y_bf16 = y_dtype == KXW4_BF16 ? 1 : 0;
+    return launch_w4a4(args, as_stream(stream));
 }
 
 int kxw4_partials(const kxw4_weight_t *w, const kxw4_act_t *a, int32_t *P, void *stream) {

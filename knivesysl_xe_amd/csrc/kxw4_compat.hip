@@ -186,6 +186,19 @@ int x_gemm_w4a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as
     return kxw4_gemm(&d, &a, d_y, KXW4_F32, nullptr, offsets, segments, 0, g_stream);
 }
 
+void x_quantize_act_chunk_s4(const float *d_x, int K, int T, uint8_t *d_aq4, float *d_as4,
+                             int32_t *d_asum4) {
+    kxw4_quantize_act_s4(d_x, KXW4_F32, T, K, d_aq4, d_as4, d_asum4, g_stream);
+}
+
+int x_gemm_w4a4(const tq_qmma_weight_t *w, const uint8_t *d_aq4, const float *d_as4,
+                const int32_t *d_asum4, float *d_y, int T) {
+    if (!w || !w->s4_ready || !w->s4_k64 || !w->d_s4 || !w->d_s4_scale) return -1;
+    if (!d_aq4 || !d_as4 || !d_asum4 || !d_y || T <= 0 || (T % 8) != 0) return -2;
+    const kxw4_weight_t d = w4_of(w);
+    return kxw4_gemm_w4a4(&d, d_aq4, d_as4, d_asum4, T, d_y, KXW4_F32, nullptr, g_stream);
+}
+
 int x_gemv_qmma_prepared(const tq_qmma_weight_t *w, const float *d_x, float *d_y,
                          const float *d_residual) {
     if (!w || !d_x || !d_y) return -1;

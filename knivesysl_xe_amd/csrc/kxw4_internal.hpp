@@ -81,6 +81,22 @@ int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T,
 int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 
+// s4 activations of the W4A4 GEMM: q4 [K/128][T][64 B], scale and sum [K/64][T]
+int launch_quantize_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4, float *scale,
+                       int32_t *sum, hipStream_t st);
+
+struct W4a4Args {
+    const uint8_t *q4;                // [K/128][T][64 B] s4 tiles
+    const float *as4;                 // [K/64][T]
+    const uint8_t *codes;             // packed K64 weight, FP16|zp scales
+    const uint16_t *scales;
+    void *y;
+    const float *residual;
+    int M, K, T, y_bf16;
+    int n_tiles, t_tiles;             // set by the launcher
+};
+int launch_w4a4(W4a4Args &a, hipStream_t st);
+
 // compute units of the current device (cached per device)
 int device_cus();
 

@@ -225,6 +225,84 @@ general:
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
+// s4 activations of the W4A4 GEMM (x_quantize_act_chunk_s4,
+// kernels_dpas.cpp:1492-1498 over quantize_act_chunk_subgroup<true>,
+// 1149-1197): per (token, K64) block s = absmax/7 (1 when the max is not
+// positive), q = clamp(rint(v / s), -7, 7) and the exact code sum. One thread
+// per 8 consecutive elements: a K64 block is 8 consecutive lanes (3-step
+// shuffles) and its 8 codes pack into one dword of the s4 tile layout, where
+// chunk c (k = 128kb + 8c .. +7) of token t lands at dword
+// (kb*T + t)*16 + 4(c & 3) + (c >> 2), codes 0..3 in the low nibbles of its
+// bytes and 4..7 in the high nibbles. Scales and sums are [K/64][T].
+template <int P>
+__global__ __launch_bounds__(256) void quantize_s4_kernel(const void *x, int T, int K, uint32_t *q4,
+                                                          float *scale, int32_t *sum) {
+    const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int cpt = K / 8;                                   // chunks per token, a multiple of 16
+    const bool live = id < (size_t)T * cpt;                  // 8-lane groups are live or dead as a whole
+    const int t = live ? (int)(id / cpt) : 0;
+    const int idx = live ? (int)(id % cpt) : 0;
+    float v[8];
+    if (live) {
+        if constexpr (P == kLoadBF16) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + (size_t)t * K + 8 * idx);
+            const uint32_t h[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = __uint_as_float(h[j] << 16);
+                v[2 * j + 1] = __uint_as_float(h[j] & 0xFFFF0000u);
+            }
+        } else {
+            const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + (size_t)t * K + 8 * idx);
+            const float4 x0 = src[0], x1 = src[1];
+            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    const float s = (mx > 0.0f) ? (mx / 7.0f) : 1.0f;
+    uint32_t w = 0;
+    int sm = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = (int)clampf(rintf(v[j] / s), -7.0f, 7.0f);
+        sm += q;
+        w |= (uint32_t)(q & 0xF) << (j < 4 ? 8 * j : 8 * (j - 4) + 4);
+    }
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    sm += __shfl_xor(sm, 4, 64);
+    if (live) {
+        const int kb = idx >> 4, c = idx & 15;
+        q4[((size_t)kb * T + t) * 16 + 4 * (c & 3) + (c >> 2)] = w;
+        if ((idx & 7) == 0) {
+            const size_t o = (size_t)(idx >> 3) * T + t;
+            scale[o] = s;
+            sum[o] = sm;
+        }
+    }
+}
+
+int launch_quantize_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4, float *scale,
+                       int32_t *sum, hipStream_t st) {
+    const size_t threads = (size_t)T * (K / 8);
+    const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+    uint32_t *q = reinterpret_cast<uint32_t *>(q4);
+    if (x_dtype == 1)
+        hipLaunchKernelGGL((quantize_s4_kernel<kLoadBF16>), grid, block, 0, st, x, T, K, q, scale, sum);
+    else
+        hipLaunchKernelGGL((quantize_s4_kernel<kLoadF32>), grid, block, 0, st, x, T, K, q, scale, sum);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
 int launch_quantize(const void *x, int x_dtype, int T, int K, int block, int8_t *q,
                     float *scale, int32_t *sum, hipStream_t st) {
     QuantArgs a{x, nullptr, nullptr, nullptr, q, scale, sum, T, K, 0.0f};

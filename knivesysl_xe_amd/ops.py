@@ -15,6 +15,8 @@ of the reference's library-global scratch:
     x_gemv_w4a8_fanout                gemv_fanout
     x_gemm_w4a8                       gemm
     (one launch for gate+up)          gemm_fanout
+    x_quantize_act_chunk_s4           quantize_act_s4
+    x_gemm_w4a4                       gemm_w4a4
 
 Torch provides device memory and the current stream only; every kernel is
 the HIP code in libkxw4.so, reached through ctypes. Tensors must live on a
@@ -173,6 +175,47 @@ def quantize_act(x: torch.Tensor, block: int = 0, out: Optional[QuantAct] = None
     return a
 
 
+@dataclass
+class QuantActS4:
+    """s4 activations of the W4A4 GEMM: codes q4 [K/128][T][64] uint8 in the
+    packed-weight nibble order, scale [K/64][T] f32 and exact code sums
+    [K/64][T] i32 (the reference's as4/asum4 layout)."""
+    T: int
+    K: int
+    q4: torch.Tensor
+    scale: torch.Tensor
+    sum: torch.Tensor
+
+    @classmethod
+    def empty(cls, T: int, K: int, device="cuda") -> "QuantActS4":
+        q4 = torch.empty(K // 128, T, 64, dtype=torch.uint8, device=device)
+        scale = torch.empty(K // 64, T, dtype=torch.float32, device=device)
+        s = torch.empty(K // 64, T, dtype=torch.int32, device=device)
+        return cls(T, K, q4, scale, s)
+
+
+def quantize_act_s4(x: torch.Tensor, out: Optional[QuantActS4] = None) -> QuantActS4:
+    """Quantize [T][K] f32/bf16 activations to s4 (per (token, K64) absmax/7);
+    `out` (same T, K) is reused when given."""
+    T, K = x.shape
+    if out is not None and (out.T, out.K) != (T, K):
+        raise ValueError("out does not match the activation shape")
+    a = out if out is not None else QuantActS4.empty(T, K, x.device)
+    check("kxw4_quantize_act_s4", lib().kxw4_quantize_act_s4(
+        _ptr(x), _dtype_code(x.dtype), T, K, _ptr(a.q4), _ptr(a.scale), _ptr(a.sum), _stream()))
+    return a
+
+
+def s4_codes_natural(a: QuantActS4) -> torch.Tensor:
+    """[T][K] int8 codes in K order (inverse of the tile nibble order)."""
+    b = a.q4.view(a.K // 128, a.T, 4, 4, 4)                  # [kb][t][g][i][byte]
+    lo = (b & 0xF).to(torch.int8)
+    hi = (b >> 4).to(torch.int8)
+    nib = torch.cat([lo, hi], dim=-1)                        # [kb][t][g][i][b]
+    nib = torch.where(nib >= 8, nib - 16, nib)
+    return nib.permute(1, 0, 3, 2, 4).reshape(a.T, a.K).contiguous()   # k = 128kb + 32i + 8g + b
+
+
 def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor, block: int = 32, keep_hidden=True):
     T, K = gate.shape
     a = QuantAct.empty(T, K, block, gate.device)
@@ -253,6 +296,17 @@ def gemm_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offset
                                                      _dtype_code(dtype), off, nseg,
                                                      forced_splits, _stream()))
     return ys
+
+
+def gemm_w4a4(w: W4Weight, a: QuantActS4, dtype=torch.float32, residual=None,
+              out=None) -> torch.Tensor:
+    """W4A4 GEMM of s4 activations against a K64 weight with FP16|zp scales."""
+    y = _out(a.T, w.M, dtype, a.q4.device, out)
+    wc = w.c()
+    check("kxw4_gemm_w4a4", lib().kxw4_gemm_w4a4(
+        C.byref(wc), _ptr(a.q4), _ptr(a.scale), _ptr(a.sum), a.T, _ptr(y), _dtype_code(dtype),
+        _ptr(residual), _stream()))
+    return y
 
 
 def partials(w: W4Weight, a: QuantAct) -> torch.Tensor:

@@ -7,7 +7,9 @@ imports it.
 Arrays follow the reference's names: a weight is codes[M][K] (int4 values held
 in int8) with scales[M][K/group] (uint16 FP16 bits, optionally carrying the
 zero point in the low nibble); activations are q[T][K] int8 with
-scale[T][K/32] (block 32) or [T] (per token) and sum[T][K/32].
+scale[T][K/32] (block 32) or [T] (per token) and sum[T][K/32]; s4 activations
+of the W4A4 GEMM are q[T][K] codes in [-7, 7] with scale and sum [T][K/64]
+(block 64).
 """
 from __future__ import annotations
 
@@ -66,6 +68,7 @@ def lib():
             "orc_f16_to_f32_n": (None, [P, P, C.c_size_t]),
             "orc_f32_to_bf16_n": (None, [P, P, C.c_size_t]),
             "orc_quantize_act": (C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P, P]),
+            "orc_quantize_act_s4": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
             "orc_silu_mul": (None, [P, P, P, C.c_int]),
             "orc_rmsnorm": (None, [P, P, C.c_int, C.c_float, P]),
             "orc_fit_int4_asym": (C.c_uint16, [P, C.c_int, C.c_int, C.c_int, P]),
@@ -136,6 +139,19 @@ def quantize_act(x, block: int):
     rc = lib().orc_quantize_act(_ptr(x), T, K, block, _ptr(q), _ptr(scale), _ptr(s))
     if rc:
         raise ValueError(f"orc_quantize_act rc={rc}")
+    return q, scale, s
+
+
+def quantize_act_s4(x):
+    """x[T][K] fp32 -> (q[T][K] int8 in [-7, 7], scale[T][K/64], sum[T][K/64])."""
+    x = _c(x, np.float32)
+    T, K = x.shape
+    q = np.empty((T, K), np.int8)
+    scale = np.empty((T, K // 64), np.float32)
+    s = np.empty((T, K // 64), np.int32)
+    rc = lib().orc_quantize_act_s4(_ptr(x), T, K, _ptr(q), _ptr(scale), _ptr(s))
+    if rc:
+        raise ValueError(f"orc_quantize_act_s4 rc={rc}")
     return q, scale, s
 
 
@@ -236,7 +252,7 @@ def partials(codes, scales, group, scale_enc, q, scale, asum, block) -> np.ndarr
     q, scale = _c(q, np.int8), _c(scale, np.float32)
     asum = None if asum is None else _c(asum, np.int32)
     w, a = _structs(codes, scales, group, scale_enc, q, scale, asum, block)
-    unit = 32 if block == 32 else group
+    unit = 32 if block == 32 else 64 if block == 64 else group
     P = np.empty((q.shape[0], codes.shape[0], codes.shape[1] // unit), np.int32)
     rc = lib().orc_partials(C.byref(w), C.byref(a), _ptr(P))
     if rc:

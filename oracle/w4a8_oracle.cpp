@@ -165,6 +165,31 @@ int orc_quantize_act(const float *x, int T, int K, int block, int8_t *q,
     return 0;
 }
 
+// x_quantize_act_chunk_s4 (kernels_dpas.cpp:1492-1498 over
+// quantize_act_chunk_subgroup<true>, 1149-1197): per (token, K64) block
+// s = absmax/7 (1 when the block max is not positive), q = clamp(rint(v/s),
+// -7, 7), and the exact code sum of the block. Codes are natural order
+// [T][K]; scales and sums [T][K/64].
+int orc_quantize_act_s4(const float *x, int T, int K, int8_t *q, float *scale, int32_t *sum) {
+    if (!x || !q || !scale || !sum || T <= 0 || K <= 0 || (K % 64) != 0) return -1;
+    for (int t = 0; t < T; ++t)
+        for (int b = 0; b < K / 64; ++b) {
+            const float *v = x + (size_t)t * K + (size_t)b * 64;
+            int8_t *qb = q + (size_t)t * K + (size_t)b * 64;
+            float mx = -INFINITY;
+            for (int j = 0; j < 64; ++j) mx = std::fmax(mx, std::fabs(v[j]));
+            const float s = (mx > 0.0f) ? (mx / 7.0f) : 1.0f;
+            int32_t sm = 0;
+            for (int j = 0; j < 64; ++j) {
+                qb[j] = (int8_t)(int32_t)clampf(std::rint(v[j] / s), -7.0f, 7.0f);
+                sm += qb[j];
+            }
+            scale[(size_t)t * (K / 64) + b] = s;
+            sum[(size_t)t * (K / 64) + b] = sm;
+        }
+    return 0;
+}
+
 // kernels_dpas.cpp:197-199 (quantize_act_s8<true>): v = (g/(1+exp(-g)))*u.
 void orc_silu_mul(const float *gate, const float *up, float *out, int n) {
     for (int i = 0; i < n; ++i) {
@@ -360,14 +385,20 @@ int orc_segment_splits(const int *offsets, int segments, int T, int M, int K, in
 // ---- projection -----------------------------------------------------------
 
 static int unit_of(const orc_weight_t *w, const orc_act_t *a) {
-    return a->block == 32 ? 32 : w->group;
+    return a->block == 32 ? 32 : a->block == 64 ? 64 : w->group;
 }
+
+// K extent of one activation scale / code-sum block
+static int act_block_of(const orc_act_t *a) { return a->block == 64 ? 64 : 32; }
 
 static int check_args(const orc_weight_t *w, const orc_act_t *a) {
     if (!w || !a || !w->codes || !w->scales || !a->q || !a->scale) return -1;
     if (w->M <= 0 || w->M % 16 || w->K <= 0 || w->K % 128 || w->K != a->K) return -2;
     if (w->group != 32 && w->group != 64 && w->group != 128) return -2;
-    if (a->block != 0 && a->block != 32) return -2;
+    if (a->block != 0 && a->block != 32 && a->block != 64) return -2;
+    // block 64 = s4 activations of the W4A4 GEMM (kernels_dpas.cpp:1503-1504):
+    // K64-tier weights with FP16|zp scales only
+    if (a->block == 64 && (w->group != 64 || w->scale_enc != ORC_SCALE_FP16_ZP4)) return -1;
     if (w->scale_enc == ORC_SCALE_FP16_ZP4 && !a->sum) return -1;
     if (w->scale_enc != ORC_SCALE_FP16 && w->scale_enc != ORC_SCALE_FP16_ZP4) return -2;
     return 0;
@@ -386,9 +417,10 @@ static inline int32_t unit_partial(const orc_weight_t *w, const orc_act_t *a, in
     if (w->scale_enc == ORC_SCALE_FP16_ZP4) {
         const int g = (u * unit) / w->group;
         z = sext4(w->scales[(size_t)n * (K / w->group) + g]);
+        const int ab = act_block_of(a);
         int32_t s = 0;
-        for (int b = (u * unit) / 32; b < ((u + 1) * unit) / 32; ++b)
-            s += a->sum[(size_t)t * (K / 32) + b];
+        for (int b = (u * unit) / ab; b < ((u + 1) * unit) / ab; ++b)
+            s += a->sum[(size_t)t * (K / ab) + b];
         d -= z * s;
     }
     *zero_point = z;
@@ -430,6 +462,8 @@ int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
     if (variant != ORC_VAR_GEMV && variant != ORC_VAR_FANOUT && variant != ORC_VAR_GEMM)
         return -2;
     if (variant == ORC_VAR_FANOUT && residual) return -2;
+    // W4A4: the GEMM variant, one chain per output (kernels_dpas.cpp:1540-1568)
+    if (a->block == 64 && variant != ORC_VAR_GEMM) return -2;
     const int M = w->M, K = w->K, T = a->T;
     if (row_begin < 0 || row_end > M || row_begin > row_end) return -2;
     const int unit = unit_of(w, a), Nu = K / unit, G = K / w->group;
@@ -462,7 +496,7 @@ int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
                         if (per_token) {
                             acc = contract ? std::fma(p, ws, acc) : acc + p * ws;
                         } else {
-                            const float as = a->scale[(size_t)t * (K / 32) + u];
+                            const float as = a->scale[(size_t)t * (K / act_block_of(a)) + u];
                             if (variant == ORC_VAR_GEMM) {
                                 const float wa = ws * as;
                                 acc = contract ? std::fma(p, wa, acc) : acc + p * wa;

@@ -16,16 +16,25 @@
  *                    point in its low nibble (ORC_SCALE_FP16_ZP4).
  *   config mode    : per-token activation scale (block 0), weight group 64 or
  *                    128, plain FP16 scale, zero point 0 (ORC_SCALE_FP16).
+ *   W4A4 mode      : s4 activations (block 64: codes in [-7, 7], one FP32
+ *                    scale and one code sum per (token, K64)), K64 weights
+ *                    with FP16|zp scales, the GEMM variant (x_gemm_w4a4,
+ *                    kernels_dpas.cpp:1500-1571).
  * The int32 "unit" partial is taken over min(weight group, activation block);
  * it is exact in every mode.
  *
  * Pinning (what checks each function against something other than itself):
  *   conversions      numpy IEEE RNE, all 65536 FP16 codes, BF16 ties
  *   quantizers       golden vectors written from numpy (the reference's
- *                    chunk_quant_bench edge pattern), round-half-even ties
+ *                    chunk_quant_bench edge pattern), round-half-even ties;
+ *                    the s4 quantizer by its closed-form properties (|q| <= 7,
+ *                    the absmax element at +-7, |v - q s| <= s/2, zero and
+ *                    NaN blocks, exact sums)
  *   partials         numpy int64 matrix products
  *   projection       exact-rational cases, hand-derived accumulation-order
- *                    cases per variant, all-ones => K, GEMM-vs-GEMV cosine gate
+ *                    cases per variant, all-ones => K, GEMM-vs-GEMV cosine gate;
+ *                    W4A4: all-ones => K, zero-point cases, and the reference's
+ *                    W4A4-vs-W4A8 cosine gate (kernels_dpas.cpp:2346-2409)
  *   split plans      the reference's stated values for the BASELINE shapes
  *   orc_e2m3         the OCP FP6 E2M3 closed form
  *   orc_e2m3_code_at parity unpinned beyond structure: tests show every
@@ -75,6 +84,9 @@ void orc_f32_to_bf16_n(const float *x, uint16_t *b, size_t n);
  * sum[T][K/32] (exact int32 code sums per K32; may be NULL). */
 int orc_quantize_act(const float *x, int T, int K, int block, int8_t *q,
                      float *scale, int32_t *sum);
+/* x[T][K] fp32 -> s4 codes q[T][K] (int8 holding [-7, 7]), scale and code
+ * sum [T][K/64] (x_quantize_act_chunk_s4). */
+int orc_quantize_act_s4(const float *x, int T, int K, int8_t *q, float *scale, int32_t *sum);
 /* out[i] = (g/(1+exp(-g))) * up[i] */
 void orc_silu_mul(const float *gate, const float *up, float *out, int n);
 /* out[i] = in[i] * rsqrt(mean(in^2)+eps) * (1 + bf16(w[i])) */
@@ -113,10 +125,10 @@ typedef struct {
 } orc_weight_t;
 
 typedef struct {
-    int T, K, block;         /* block: 32 or 0 (per token) */
+    int T, K, block;         /* block: 32, 64 (s4, W4A4) or 0 (per token) */
     const int8_t *q;         /* [T][K] */
-    const float *scale;      /* [T][K/32] or [T] */
-    const int32_t *sum;      /* [T][K/32] */
+    const float *scale;      /* [T][K/block] or [T] */
+    const int32_t *sum;      /* [T][K/32], or [T][K/64] for block 64 */
 } orc_act_t;
 
 /* Exact int32 unit partials P[T][M][K/unit]. */

@@ -237,6 +237,56 @@ int main() {
     check(same_bits(host_copy(dyt, (size_t)T * 1024), oracle_project(s32, xt, T, ORC_VAR_GEMM, spt, nullptr)),
           "x_gemm_w4a8 packed == oracle (per-segment splits)");
 
+    // ---- W4A4: s4 chunk quantization + W4A4 GEMM on the K64 weight ----------
+    {
+        const int T4 = 40, K = 2048, M = 512;
+        uint8_t *daq4;
+        float *das4, *dy4;
+        int32_t *dsum4;
+        HIPCHECK(hipMalloc(&daq4, (size_t)T4 * K / 2));
+        HIPCHECK(hipMalloc(&das4, (size_t)T4 * (K / 64) * sizeof(float)));
+        HIPCHECK(hipMalloc(&dsum4, (size_t)T4 * (K / 64) * sizeof(int32_t)));
+        HIPCHECK(hipMalloc(&dy4, (size_t)T4 * M * sizeof(float)));
+        x_quantize_act_chunk_s4(dxt, K, T4, daq4, das4, dsum4);
+        std::vector<int8_t> q((size_t)T4 * K);
+        std::vector<float> sc((size_t)T4 * (K / 64));
+        std::vector<int32_t> sm((size_t)T4 * (K / 64));
+        orc_quantize_act_s4(xt.data(), T4, K, q.data(), sc.data(), sm.data());
+        // device layout: codes [K/128][T][64 B] tile order, scale/sum [K/64][T]
+        const std::vector<uint8_t> hq = host_copy(daq4, (size_t)T4 * K / 2);
+        const std::vector<float> hs = host_copy(das4, sc.size());
+        const std::vector<int32_t> hsum = host_copy(dsum4, sm.size());
+        bool codes_ok = true, ss_ok = true;
+        for (int t = 0; t < T4; ++t)
+            for (int k = 0; k < K; ++k) {
+                const int kb = k / 128, kk = k % 128, i = kk / 32, g = (kk / 8) % 4, b = kk % 8;
+                const uint8_t byte = hq[((size_t)kb * T4 + t) * 64 + 16 * g + 4 * i + (b & 3)];
+                const int nib = b < 4 ? (byte & 0xF) : (byte >> 4);
+                codes_ok &= (nib >= 8 ? nib - 16 : nib) == q[(size_t)t * K + k];
+            }
+        for (int t = 0; t < T4; ++t)
+            for (int u = 0; u < K / 64; ++u) {
+                ss_ok &= std::memcmp(&hs[(size_t)u * T4 + t], &sc[(size_t)t * (K / 64) + u], 4) == 0;
+                ss_ok &= hsum[(size_t)u * T4 + t] == sm[(size_t)t * (K / 64) + u];
+            }
+        check(codes_ok, "x_quantize_act_chunk_s4 codes == oracle");
+        check(ss_ok, "x_quantize_act_chunk_s4 scales and sums == oracle ([K/64][T])");
+        check(x_gemm_w4a4(&w64, daq4, das4, dsum4, dy4, T4) == 0, "x_gemm_w4a4 returns 0");
+        orc_act_t a{T4, K, 64, q.data(), sc.data(), sm.data()};
+        orc_weight_t ow = oracle_weight(s64);
+        std::vector<float> y((size_t)T4 * M, 0.0f);
+        const std::vector<int> one(T4, 1);
+        orc_project(&ow, &a, ORC_VAR_GEMM, one.data(), 1, nullptr, 0, y.data(), 0, M);
+        check(same_bits(host_copy(dy4, (size_t)T4 * M), y), "x_gemm_w4a4 == oracle");
+        check(x_gemm_w4a4(&w32, daq4, das4, dsum4, dy4, T4) == -1, "x_gemm_w4a4 on a K32 weight = -1");
+        check(x_gemm_w4a4(&w64, daq4, das4, dsum4, dy4, 36) == -2, "x_gemm_w4a4 T % 8 != 0 = -2");
+        check(x_gemm_w4a4(&w64, daq4, das4, nullptr, dy4, T4) == -2, "x_gemm_w4a4 without sums = -2");
+        HIPCHECK(hipFree(daq4));
+        HIPCHECK(hipFree(das4));
+        HIPCHECK(hipFree(dsum4));
+        HIPCHECK(hipFree(dy4));
+    }
+
     // ---- argument checks keep the reference's codes ------------------------
     tq_qmma_weight_t bad;
     std::memset(&bad, 0, sizeof(bad));

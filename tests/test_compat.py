@@ -41,6 +41,9 @@ def test_library_exports_reference_signatures():
                                        "int const*, float*, int, int const*, int")
     assert exported["x_gemv_w4a8_fanout"] == "tq_qmma_weight_t const* const*, float* const*, int"
     assert exported["x_rmsnorm_quant"] == "float*, float const*, unsigned short const*, int, float"
+    assert exported["x_gemm_w4a4"] == ("tq_qmma_weight_t const*, unsigned char const*, float const*, "
+                                       "int const*, float*, int")
+    assert exported["x_quantize_act_chunk_s4"] == "float const*, int, int, unsigned char*, float*, int*"
     assert "kxw4_compat_set_stream" in out
 
 

@@ -373,3 +373,118 @@ def test_gemm_agrees_with_gemv_reference_gate():
         a, b = ref[t].astype(np.float64), got[t].astype(np.float64)
         assert a @ b / np.sqrt((a @ a) * (b @ b)) >= 0.9999
     assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-3)) < 1e-3
+
+
+# ---- W4A4: s4 activation quantizer and the W4A4 GEMM arithmetic -------------
+
+def test_s4_quantizer_known_answers():
+    # x_quantize_act_chunk_s4 (kernels_dpas.cpp:1149-1197, S4): per (token, K64)
+    # s = absmax/7, q = clamp(rint(v/s), -7, 7). With absmax 7 the scale is 1 and
+    # the codes are rint of the values themselves: ties go to even.
+    x = np.zeros((2, 128), np.float32)
+    x[0, :8] = [7.0, 0.5, 1.5, 2.5, -2.5, -0.5, 3.49, -6.51]
+    x[0, 64:66] = [-14.0, 5.0]          # block 1: s = 2, 5/2 = 2.5 -> 2
+    x[1, 3] = np.nan                     # block 0 of token 1: NaN beside zeros
+    x[1, 64 + 9] = 1e-30                 # tiny absmax, s = 1e-30/7
+    q, s, sm = O.quantize_act_s4(x)
+    assert s[0, 0] == 1.0 and s[0, 1] == 2.0
+    assert list(q[0, :8]) == [7, 0, 2, 2, -2, 0, 3, -7]
+    assert list(q[0, 64:66]) == [-7, 2] and not q[0, 66:].any()
+    assert sm[0, 0] == 7 + 0 + 2 + 2 - 2 + 0 + 3 - 7 and sm[0, 1] == -5
+    # NaN is ignored by the max (fmax) and lands on the low clamp bound (sycl
+    # clamp = fmin(fmax(x, lo), hi)); an all-zero max gives scale 1
+    assert s[1, 0] == 1.0 and q[1, 3] == -7 and sm[1, 0] == -7
+    assert s[1, 1] == np.float32(1e-30) / np.float32(7) and q[1, 64 + 9] == 7
+
+
+def test_s4_quantizer_invariants():
+    rng = np.random.default_rng(21)
+    T, K = 5, 640
+    x = (rng.standard_normal((T, K)) * np.exp2(rng.integers(-20, 20, (T, 1)))).astype(np.float32)
+    x[2, 64:128] = 0.0
+    q, s, sm = O.quantize_act_s4(x)
+    assert np.abs(q).max() <= 7
+    xb = x.reshape(T, K // 64, 64)
+    qb = q.reshape(T, K // 64, 64).astype(np.int64)
+    mx = np.abs(xb).max(axis=2)
+    want_s = np.where(mx > 0, mx / np.float32(7), np.float32(1)).astype(np.float32)
+    assert np.array_equal(s, want_s)
+    assert np.array_equal(sm, qb.sum(axis=2))
+    # the absmax element maps to +-7; every code is within half a step
+    arg = np.abs(xb).argmax(axis=2)
+    top = np.take_along_axis(qb, arg[..., None], axis=2)[..., 0]
+    assert np.all((np.abs(top) == 7) | (mx == 0))
+    err = np.abs(xb.astype(np.float64) - qb * s[..., None].astype(np.float64))
+    assert np.all(err <= 0.5 * s[..., None] * (1 + 1e-6))
+    assert not q[2, 64:128].any() and s[2, 1] == 1.0
+
+
+def w4a4_weight(rng, M, K):
+    codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    mags = (np.abs(rng.standard_normal((M, K // 64))) * 0.02).astype(np.float16).view(np.uint16)
+    scales = ((mags & 0xFFF0) | (rng.integers(-8, 8, mags.shape) & 0xF)).astype(np.uint16)
+    return codes, scales
+
+
+def test_w4a4_all_ones_gives_K():
+    # xpu/probe/w4a4_gemm_probe.cpp:13-17 (s4 x s4 arm)
+    M, K, T = 32, 512, 8
+    codes = np.ones((M, K), np.int8)
+    scales = np.full((M, K // 64), 0x3C00, np.uint16)
+    q, s, sm = O.quantize_act_s4(np.ones((T, K), np.float32) * 7)
+    assert np.all(q == 7) and np.all(s == 1.0)
+    y = O.project(codes, scales, 64, O.SCALE_FP16_ZP4, q // 7, s, sm // 7, 64, O.VAR_GEMM, 1)
+    assert np.all(y == K)
+
+
+def test_w4a4_zero_point_exact_case():
+    # exact-rational case: scales 2^-k and codes small enough that every FP32
+    # step is exact, so y must equal the int64 product sum_u (w - zp_u) . a_u
+    # * ws_u * as_u, pinning the zero-point sign and the per-K64 sum indexing
+    rng = np.random.default_rng(22)
+    M, K, T = 48, 384, 8
+    codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    zp = rng.integers(-8, 8, (M, K // 64))
+    ws_exp = rng.integers(-4, 2, (M, K // 64))
+    scales = ((np.exp2(ws_exp).astype(np.float16).view(np.uint16) & 0xFFF0) | (zp & 0xF)).astype(np.uint16)
+    q = rng.integers(-7, 8, (T, K)).astype(np.int8)
+    sm = q.reshape(T, K // 64, 64).sum(axis=2).astype(np.int32)
+    s = np.exp2(rng.integers(-3, 3, (T, K // 64))).astype(np.float32)
+    y = O.project(codes, scales, 64, O.SCALE_FP16_ZP4, q, s, sm, 64, O.VAR_GEMM, 1)
+    w = codes.reshape(M, K // 64, 64).astype(np.int64) - zp[..., None]
+    a = q.reshape(T, K // 64, 64).astype(np.int64)
+    d = np.einsum("muk,tuk->tmu", w, a)
+    want = (d * np.exp2(ws_exp)[None] * s[:, None, :]).sum(axis=2)
+    assert np.array_equal(y, want.astype(np.float32))
+
+
+def test_w4a4_agrees_with_w4a8_gemv_gate():
+    # the reference's gate qwn_gemm_w4a4_check (kernels_dpas.cpp:2335-2409): the
+    # W4A4 GEMM against the W4A8 GEMV on the same K64 weight, worst token-row
+    # cosine >= 0.995 on the deterministic gate input, at the gate's K = 5120
+    # (the s4 noise it is sized for; the reference measured 0.9962-0.9963)
+    rng = np.random.default_rng(23)
+    M, K, T = 256, 5120, 8
+    codes, scales = w4a4_weight(rng, M, K)
+    x = gemm_check_input(T, K)
+    q8, s8, sm8 = O.quantize_act(x, 32)
+    ref = O.project(codes, scales, 64, 1, q8, s8, sm8, 32, O.VAR_GEMV, O.gemv_splits(M // 16))
+    q4, s4, sm4 = O.quantize_act_s4(x)
+    got = O.project(codes, scales, 64, 1, q4, s4, sm4, 64, O.VAR_GEMM, 1)
+    cos = [ref[t].astype(np.float64) @ got[t] /
+           np.sqrt((ref[t].astype(np.float64) @ ref[t]) * (got[t].astype(np.float64) @ got[t]))
+           for t in range(T)]
+    assert min(cos) >= 0.995 and min(cos) < 0.99999, cos
+
+
+def test_w4a4_rejects_other_tiers_and_variants():
+    rng = np.random.default_rng(24)
+    M, K, T = 32, 256, 8
+    codes, scales = w4a4_weight(rng, M, K)
+    q, s, sm = O.quantize_act_s4(rng.standard_normal((T, K)).astype(np.float32))
+    with pytest.raises(ValueError, match="rc=-2"):
+        O.project(codes, scales, 64, 1, q, s, sm, 64, O.VAR_GEMV, 1)
+    with pytest.raises(ValueError, match="rc=-1"):
+        O.project(codes, scales[:, ::2].copy(), 128, 1, q, s, sm, 64, O.VAR_GEMM, 1)
+    with pytest.raises(ValueError, match="rc=-1"):
+        O.project(codes, scales & 0xFFF0, 64, 0, q, s, sm, 64, O.VAR_GEMM, 1)
