@@ -183,6 +183,59 @@ def measure(cfg, steps, warmup, eager=False):
     return res
 
 
+def measure_w4a4(cfg, steps, warmup, eager=False):
+    """The W4A4 GEMM (x_gemm_w4a4, the reference's default prefill dispatch for
+    K64 weights) on a K64 config's shape: the config's codes, its FP16 scales
+    with the low nibble replaced by a seeded zero point (FP16|zp encoding),
+    and its BF16 activations quantized to s4 outside the timed region."""
+    import torch
+    from knivesysl_xe_amd import ops, workloads
+    from oracle import oracle as O
+    assert cfg.group == 64 and len(cfg.rows) == 1 and not cfg.segments
+    inp = workloads.generate(cfg, 0)
+    rng = np.random.default_rng(1)
+    codes = inp.codes[0]
+    scales = ((inp.scales[0] & 0xFFF0) | (rng.integers(-8, 8, inp.scales[0].shape) & 0xF)).astype(np.uint16)
+    w = ops.W4Weight.from_codes(torch.from_numpy(codes).cuda(),
+                                torch.from_numpy(scales.view(np.int16)).cuda(), 64, O.SCALE_FP16_ZP4)
+    x = torch.from_numpy(inp.x_bf16.view(np.int16)).cuda().view(torch.bfloat16)
+    act = ops.quantize_act_s4(x)
+    dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
+    out = torch.empty(cfg.tokens, w.M, dtype=dt, device="cuda")
+    copies, rot_bytes = make_copies([w])
+    run = lambda ws: ops.gemm_w4a4(ws[0], act, dt, out=out)
+    secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
+    run(copies[0])
+    torch.cuda.synchronize()
+    q, s, sm = O.quantize_act_s4(workloads.bf16_bits_to_f32(inp.x_bf16))
+    ref = O.project(codes, scales, 64, O.SCALE_FP16_ZP4, q, s, sm, 64, O.VAR_GEMM, 1,
+                    out_bf16=cfg.out_bf16, rows=(0, 512))
+    got = out[:, :512]
+    got = got.view(torch.int16).cpu().numpy().view(np.uint16) if cfg.out_bf16 \
+        else got.cpu().numpy().view(np.uint32)
+    exact = bool(np.array_equal(got, ref[:, :512].view(got.dtype)))
+    qa = ops.QuantActS4.empty(cfg.tokens, cfg.K)
+    qsecs, _ = time_graph(lambda _c: ops.quantize_act_s4(x, out=qa), [None], 20, 2)
+    per = secs / steps
+    N = sum(cfg.rows)
+    res = {
+        "kernel_us": per * 1e6,
+        "TOPS": cfg.ops() / per / 1e12,
+        "ops": cfg.ops(),
+        "bound": "mfma",
+        "bit_exact_vs_oracle_rows0_512": exact,
+        "rotated_weight_bytes": rot_bytes,
+        "quantize_s4_us": qsecs / 20 * 1e6,
+        "bytes": N * cfg.K // 2 + N * (cfg.K // 64) * 2 + cfg.tokens * cfg.K // 2 + cfg.tokens * N * 4,
+        "wall_s": wall,
+    }
+    res["GBps"] = res["bytes"] / per / 1e9
+    res["roofline_frac"] = res["TOPS"] / INT8_PEAK_TOPS
+    del copies, w, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, budget_s=10.0):
     """The oracle on the host cores over repeated full passes of `cfg`."""
     from oracle import oracle as O
@@ -246,6 +299,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="cfg0,cfg2_m1,cfg2_m512,cfg3,cfg4",
                     help="extra BASELINE configs to report ('' for none)")
+    ap.add_argument("--w4a4", default="cfg2_m512",
+                    help="K64 configs to also run through the W4A4 GEMM ('' for none)")
     ap.add_argument("--extra-steps", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
@@ -273,6 +328,12 @@ def main():
         e = extra[name]
         log(f"{name}: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, {e['TOPS']:.1f} TOPS, "
             f"frac {e['roofline_frac']:.3f}, exact={e['bit_exact_vs_oracle_rows0_512']}")
+    for name in [c for c in args.w4a4.split(",") if c]:
+        cfg = workloads.CONFIGS[name]
+        log(f"{name}_w4a4: W4A4 GEMM on the {name} shape (s4 activations, FP16|zp K64 weight)")
+        e = extra[f"{name}_w4a4"] = measure_w4a4(cfg, args.extra_steps, 5, args.eager)
+        log(f"{name}_w4a4: {e['kernel_us']:.2f} us, {e['TOPS']:.1f} TOPS, frac {e['roofline_frac']:.3f}, "
+            f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     if args.copy_mib:
         calibration_copy(args.copy_mib)
     log("cpu baseline (oracle on host cores)")
