@@ -43,8 +43,11 @@ enum {
 
 /* Scale encodings. FP16_ZP4 is the reference's packing: FP16 scale whose low
  * four mantissa bits carry a signed zero point (kernels_dpas.cpp:253-255,
- * decode 630-634). FP16 is a plain FP16 scale with zero point 0. */
-enum { KXW4_SCALE_FP16 = 0, KXW4_SCALE_FP16_ZP4 = 1 };
+ * decode 630-634). FP16 is a plain FP16 scale with zero point 0. W8 marks the
+ * W8A8 tier (kernels_dpas.cpp:346-399, 771-844, 1578-1629): int8 codes in
+ * the W8 tile layout below with a plain FP16 scale per (row, K32); group 32
+ * and block-32 activations only. */
+enum { KXW4_SCALE_FP16 = 0, KXW4_SCALE_FP16_ZP4 = 1, KXW4_SCALE_W8 = 2 };
 
 /* Element types of activations, residuals and outputs. */
 enum { KXW4_F32 = 0, KXW4_BF16 = 1 };
@@ -58,7 +61,12 @@ enum { KXW4_F32 = 0, KXW4_BF16 = 1 };
  *           b = 0..3 in the low nibbles of bytes 0..3 and b = 4..7 in the
  *           high nibbles. Nibbles are two's-complement int4.
  *   scales: [M/16][K/group][16] uint16 (row within the row-group fastest).
- * Requires M % 16 == 0, K % 128 == 0, group in {32, 64, 128}. */
+ * W8 weights (scale_enc KXW4_SCALE_W8): codes are M*K bytes, tiles of 16 rows
+ * x 128 K = 2048 bytes at (rg*(K/128) + kb)*2048; half h at byte 1024h, lane
+ * l owns bytes [1024h + 16l, +16) of row rg*16 + l%16, holding K32 units
+ * j = 2h (bytes 0..7) and 2h+1 (bytes 8..15), byte b of unit j being
+ * k = kb*128 + 32j + 8(l/16) + b (the K slots the W4 unpack produces).
+ * Requires M % 16 == 0, K % 128 == 0, group in {32, 64, 128} (32 for W8). */
 typedef struct kxw4_weight {
     int32_t M, K, group, scale_enc;
     const uint8_t *codes;
@@ -105,6 +113,20 @@ int kxw4_pack_weight(const int8_t *codes, const uint16_t *scales, int M, int K,
 int kxw4_unpack_weight(const kxw4_weight_t *w, int8_t *codes, uint16_t *scales,
                        void *stream);
 
+/* W8A8 tier: natural int8 codes [M][K] and FP16 scales [M][K/32] -> the W8
+ * tile layout (KXW4_SCALE_W8). kxw4_unpack_weight inverts it. */
+int kxw4_pack_weight_s8(const int8_t *codes, const uint16_t *scales, int M,
+                        int K, uint8_t *out_codes, uint16_t *out_scales,
+                        void *stream);
+
+/* x_w8_repack_weight (kernels_dpas.cpp:346-399, 558-575): dense-E2M3
+ * fragment payload and FP32 block scales -> int8 codes (per (row, K32):
+ * s = max(hi/127, neg/128), two least-squares refinements, FP16 scale,
+ * codes rint(w/s) clamped to [-128, 127]) in the W8 tile layout. */
+int kxw4_repack_e2m3_s8(const uint8_t *payload, const float *block_scale_inv,
+                        int scale_cols, int M, int K, uint8_t *out_codes,
+                        uint16_t *out_scales, void *stream);
+
 /* Reference DPAS layout (lane-major K32 tiles and FP16|zp scales
  * [M/16][K/group][16], kernels_dpas.cpp:294-342) -> packed layout. Scales are
  * copied bit for bit; group is 32 or 64 (s4_k64). */
@@ -142,6 +164,12 @@ int kxw4_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T,
                        int H, float eps, int block, int8_t *q, float *scale,
                        int32_t *sum, void *stream);
 
+/* x_rmsnorm_chunk (kernels_dpas.cpp:1124-1144): out[t][i] = in[t][i] *
+ * rsqrt(mean(in[t]^2) + eps) * (1 + bf16(w[i])) over T rows of H, the same
+ * rows kxw4_rmsnorm_quant writes to its `out`, without the quantizer. */
+int kxw4_rmsnorm(float *out, const float *in, const uint16_t *w, int T, int H,
+                 float eps, void *stream);
+
 /* s4 activations of the W4A4 GEMM: x_quantize_act_chunk_s4
  * (kernels_dpas.cpp:1492-1498 over 1149-1197). x[T][K] (KXW4_F32 or
  * KXW4_BF16) -> per (token, K64) block s = absmax/7 (1 when the block max is
@@ -162,13 +190,16 @@ int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4,
  * x_gemv_w4a8_prepared dispatch (1631-1680): per token row, K split in
  * `splits` parts (0 = choose_gemv_splits(M/16)), two alternating
  * accumulators per split, ordered split sum, optional FP32 residual[T][M].
- * T in [1, 64]. y is [T][M] of y_dtype. */
+ * T in [1, 64]. y is [T][M] of y_dtype. A W8 weight runs x_gemv_w8a8_core's
+ * arithmetic (kernels_dpas.cpp:771-844, the same chain with zero point 0) for
+ * T in [1, 16]. */
 int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
               const float *residual, int splits, void *stream);
 
 /* x_gemv_w4a8_fanout (kernels_dpas.cpp:945-1102): up to 4 weights with one K
  * and one group/encoding, one launch, serial accumulator, one split count
- * choose_gemv_splits(total row-groups). T in [1, 64]. */
+ * choose_gemv_splits(total row-groups). T in [1, 64]. W8 weights return
+ * KXW4_ETIER (the reference has no W8 fan-out). */
 int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
                      const kxw4_act_t *a, int y_dtype, void *stream);
 
@@ -177,7 +208,8 @@ int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
  * ordered split sum. offsets[segments+1] is host memory (NULL with
  * segments 0 for one segment); segments may have any positive length (the
  * reference requires multiples of 8). Optional FP32 residual[T][M] is added
- * after the projection. */
+ * after the projection. A W8 weight runs x_gemm_w8a8's arithmetic
+ * (kernels_dpas.cpp:1578-1629) on block-32 activations. */
 int kxw4_gemm(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
               const float *residual, const int *offsets, int segments,
               int forced_splits, void *stream);

@@ -28,8 +28,9 @@
 #include "kxw4.h"
 
 // The W4-relevant members of the reference descriptor (tq_common.hpp:49-76),
-// field names kept. Members of tiers this library does not build (d_s8,
-// e2m1, ...) are present so code that sets them compiles; they are ignored.
+// field names kept. Members of tiers this library does not build (e2m1,
+// row_major, ...) are present so code that sets them compiles; they are
+// ignored.
 typedef struct {
     int M, K, Mt, Kt;          // Mt = M/16, Kt = K/32
     float inv_scale;
@@ -48,8 +49,8 @@ typedef struct {
     int s4_ready;
     int s4_k16;
     int s4_k64;                // 1 = one scale per K64 group
-    uint8_t *d_s8;
-    uint16_t *d_s8_scale;
+    uint8_t *d_s8;             // W8A8 tier: int8 codes, kxw4.h W8 tile layout
+    uint16_t *d_s8_scale;      // [M/16][K/32][16] FP16
     int s8_ready;
 } tq_qmma_weight_t;
 
@@ -60,6 +61,9 @@ extern "C" void kxw4_compat_set_stream(void *stream);
 // d_block_scale_inv, synchronizes.
 int x_w4_repack_weight(tq_qmma_weight_t *w);
 int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode);
+// kernels_dpas.cpp:558-575: the W8A8 tier (d_s8 / d_s8_scale in the W8 tile
+// layout of kxw4.h); allocates, frees d_A and d_block_scale_inv, synchronizes.
+int x_w8_repack_weight(tq_qmma_weight_t *w);
 // kernels_dpas.cpp:220-223: one token, block 32.
 void x_quantize_act_s8(const float *d_x, int K, int8_t *d_q, float *d_scale, int32_t *d_sum);
 // kernels_dpas.cpp:1631-1680 and 846-849.
@@ -69,6 +73,8 @@ void x_prepare_gemv_act_s8(const float *d_x, int K);
 // kernels_dpas.cpp:851-855, 866-929.
 void x_silu_mul_quant(float *d_out, const float *d_gate, const float *d_up, int K);
 void x_rmsnorm_quant(float *d_out, const float *d_in, const uint16_t *d_w, int H, float eps);
+// kernels_dpas.cpp:1124-1144: T rows, no quantization.
+void x_rmsnorm_chunk(float *d_out, const float *d_in, const uint16_t *d_w, int H, int T, float eps);
 // kernels_dpas.cpp:945-1102.
 int x_gemv_w4a8_fanout(const tq_qmma_weight_t *const *ws, float *const *ys, int count);
 // kernels_dpas.cpp:1149-1207: T token rows, block 32.
@@ -85,7 +91,14 @@ void x_quantize_act_chunk_s4(const float *d_x, int K, int T, uint8_t *d_aq4, flo
 // missing operand or T % 8 != 0.
 int x_gemm_w4a4(const tq_qmma_weight_t *w, const uint8_t *d_aq4, const float *d_as4,
                 const int32_t *d_asum4, float *d_y, int T);
-// kernels_core.cpp:235-252: W4A8 when s4_ready, otherwise KXW4_ETIER.
+// kernels_dpas.cpp:1682-1725 (W8A8 GEMV on the prepared activation) and
+// 1578-1629 (W8A8 GEMM, T % 8 == 0, block-32 chunk activations).
+int x_gemv_w8a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual = nullptr);
+int x_gemv_w8a8(const tq_qmma_weight_t *w, const float *d_x, float *d_y);
+int x_gemv_w8a8_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y);
+int x_gemm_w8a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as, float *d_y, int T);
+// kernels_core.cpp:235-252: W8A8 when s8_ready, else W4A8 when s4_ready,
+// otherwise KXW4_ETIER.
 int x_gemv_qmma_prepared(const tq_qmma_weight_t *w, const float *d_x, float *d_y,
                          const float *d_residual = nullptr);
 int x_gemv_qmma_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y);

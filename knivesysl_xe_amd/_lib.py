@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkxw4.so")
 
 OK, EARG, ESHAPE, EPREP, ESPLIT, ETIER, EHIP = 0, -1, -2, -3, -4, -5, -6
-SCALE_FP16, SCALE_FP16_ZP4 = 0, 1
+SCALE_FP16, SCALE_FP16_ZP4, SCALE_W8 = 0, 1, 2
 F32, BF16 = 0, 1
 
 
@@ -40,11 +40,14 @@ SIGNATURES = {
     "kxw4_gemm_splits": (I, [I, I, I, I]),
     "kxw4_pack_weight": (I, [P, P, I, I, I, P, P, P]),
     "kxw4_unpack_weight": (I, [WP, P, P, P]),
+    "kxw4_pack_weight_s8": (I, [P, P, I, I, P, P, P]),
+    "kxw4_repack_e2m3_s8": (I, [P, P, I, I, I, P, P, P]),
     "kxw4_import_ref_weight": (I, [P, P, I, I, I, P, P, P]),
     "kxw4_repack_e2m3": (I, [P, P, I, I, I, I, P, P, P]),
     "kxw4_quantize_act": (I, [P, I, I, I, I, P, P, P, P]),
     "kxw4_silu_mul_quant": (I, [P, P, P, I, I, I, P, P, P, P]),
     "kxw4_rmsnorm_quant": (I, [P, P, P, I, I, F, I, P, P, P, P]),
+    "kxw4_rmsnorm": (I, [P, P, P, I, I, F, P]),
     "kxw4_quantize_act_s4": (I, [P, I, I, I, P, P, P, P]),
     "kxw4_gemv": (I, [WP, AP, P, I, P, I, P]),
     "kxw4_gemv_fanout": (I, [C.POINTER(WP), C.POINTER(P), I, AP, I, P]),

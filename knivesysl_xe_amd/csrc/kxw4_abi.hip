@@ -22,7 +22,11 @@ bool valid_shape(int M, int K, int group) {
 int check_weight(const kxw4_weight_t *w) {
     if (!w || !w->codes || !w->scales) return KXW4_EARG;
     if (!valid_shape(w->M, w->K, w->group)) return KXW4_ESHAPE;
-    if (w->scale_enc != KXW4_SCALE_FP16 && w->scale_enc != KXW4_SCALE_FP16_ZP4) return KXW4_ETIER;
+    if (w->scale_enc != KXW4_SCALE_FP16 && w->scale_enc != KXW4_SCALE_FP16_ZP4 &&
+        w->scale_enc != KXW4_SCALE_W8)
+        return KXW4_ETIER;
+    // the W8A8 tier keeps one scale per K32 (kernels_dpas.cpp:346-399)
+    if (w->scale_enc == KXW4_SCALE_W8 && w->group != 32) return KXW4_ESHAPE;
     return KXW4_OK;
 }
 
@@ -30,6 +34,8 @@ int check_act(const kxw4_act_t *a, int K, int scale_enc) {
     if (!a || !a->q || !a->scale) return KXW4_ESHAPE;
     if (a->K != K || a->T <= 0 || (a->block != 0 && a->block != 32)) return KXW4_ESHAPE;
     if (scale_enc == KXW4_SCALE_FP16_ZP4 && !a->sum) return KXW4_EPREP;
+    // W8A8 runs on block-32 activations only (kernels_dpas.cpp:771-844, 1578-1629)
+    if (scale_enc == KXW4_SCALE_W8 && a->block != 32) return KXW4_EARG;
     return KXW4_OK;
 }
 
@@ -45,6 +51,7 @@ void fill_act(Args &args, const kxw4_act_t *a, int group, int scale_enc, int y_d
     args.group = group;
     args.block = a->block;
     args.scale_enc = scale_enc;
+    args.w8 = scale_enc == KXW4_SCALE_W8 ? 1 : 0;
     args.y_bf16 = y_dtype == KXW4_BF16 ? 1 : 0;
 }
 
@@ -119,7 +126,9 @@ int gemm_common(const kxw4_weight_t *const *ws, void *const *ys, int count, cons
         DecodeArgs args{};
         fill_plan(args, ws, ys, count, a, y_dtype, residual, dbg, ends, splits, nseg);
         args.variant = kVarGemm;
-        return launch_decode(args, dbg != nullptr, st);
+        const int r = launch_decode(args, dbg != nullptr, st);
+        // W8 shapes the row-wave kernel does not take run on the GEMM path
+        if (!(args.w8 && r == 1)) return r;
     }
     GemmArgs args{};
     fill_plan(args, ws, ys, count, a, y_dtype, residual, dbg, ends, splits, nseg);
@@ -136,7 +145,8 @@ int decode_uniform(const kxw4_weight_t *const *ws, void *const *ys, int count,
     DecodeArgs args{};
     fill_plan(args, ws, ys, count, a, y_dtype, residual, nullptr, ends, splits, 1);
     args.variant = variant;
-    return launch_decode(args, false, st);
+    const int r = launch_decode(args, false, st);
+    return r == 1 ? KXW4_ESHAPE : r;
 }
 
 }  // namespace
@@ -202,8 +212,28 @@ int kxw4_unpack_weight(const kxw4_weight_t *w, int8_t *codes, uint16_t *scales, 
     const int rc = check_weight(w);
     if (rc) return rc;
     if (!codes) return KXW4_EARG;
+    if (w->scale_enc == KXW4_SCALE_W8)
+        return launch_unpack_s8(w->codes, w->scales, w->M, w->K, codes, scales, as_stream(stream));
     return launch_unpack(w->codes, w->scales, w->M, w->K, w->group, codes, scales,
                          as_stream(stream));
+}
+
+int kxw4_pack_weight_s8(const int8_t *codes, const uint16_t *scales, int M, int K, uint8_t *out_codes,
+                        uint16_t *out_scales, void *stream) {
+    if (!codes || !scales || !out_codes || !out_scales) return KXW4_EARG;
+    if (!valid_shape(M, K, 32)) return KXW4_ESHAPE;
+    return launch_pack_s8(codes, scales, M, K, out_codes, out_scales, as_stream(stream));
+}
+
+// x_w8_repack_weight's checks (kernels_dpas.cpp:558-560): -1 missing operand,
+// -2 shape.
+int kxw4_repack_e2m3_s8(const uint8_t *payload, const float *block_scale_inv, int scale_cols, int M,
+                        int K, uint8_t *out_codes, uint16_t *out_scales, void *stream) {
+    if (!payload || !block_scale_inv || !out_codes || !out_scales || scale_cols <= 0) return KXW4_EARG;
+    if (M <= 0 || K <= 0 || M % 16 || K % 128) return KXW4_ESHAPE;
+    if (scale_cols != K / 32 && scale_cols != K / 128) return KXW4_ESHAPE;
+    return launch_repack_e2m3_s8(payload, block_scale_inv, scale_cols, M, K, out_codes, out_scales,
+                                 as_stream(stream));
 }
 
 int kxw4_import_ref_weight(const uint8_t *ref_codes, const uint16_t *ref_scales, int M, int K,
@@ -237,6 +267,13 @@ int kxw4_quantize_act(const void *x, int x_dtype, int T, int K, int block, int8_
     return launch_quantize(x, x_dtype, T, K, block, q, scale, sum, as_stream(stream));
 }
 
+int kxw4_rmsnorm(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
+                 void *stream) {
+    if (!out || !in || !w) return KXW4_EARG;
+    if (T <= 0 || H <= 0) return KXW4_ESHAPE;
+    return launch_rmsnorm(out, in, w, T, H, eps, as_stream(stream));
+}
+
 int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4, float *scale,
                          int32_t *sum, void *stream) {
     if (!x || !q4 || !scale || !sum) return KXW4_EARG;
@@ -266,6 +303,7 @@ int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
     rc = check_act(a, w->K, w->scale_enc);
     if (rc) return rc;
     if (a->T > kDecodeMaxT || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
+    if (w->scale_enc == KXW4_SCALE_W8 && a->T > 16) return KXW4_ESHAPE;
     const int S = splits ? splits : kxw4_gemv_splits(w->M / 16);
     if (!valid_split(S)) return KXW4_ESHAPE;
     const kxw4_weight_t *ws[1] = {w};
@@ -285,6 +323,7 @@ int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
             !valid_shape(w->M, w->K, w->group) || w->group != ws[0]->group ||
             w->scale_enc != ws[0]->scale_enc)
             return KXW4_ESHAPE;
+        if (w->scale_enc == KXW4_SCALE_W8) return KXW4_ETIER;   // no W8 fan-out in the reference
         groups += w->M / 16;
     }
     if (!a || !a->q || !a->scale || a->K != ws[0]->K) return KXW4_EPREP;

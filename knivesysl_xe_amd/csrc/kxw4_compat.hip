@@ -67,6 +67,19 @@ bool w4_ready(const tq_qmma_weight_t *w) {
     return w && w->s4_ready && !w->s4_k16 && w->d_s4 && w->d_s4_scale;
 }
 
+bool w8_ready(const tq_qmma_weight_t *w) { return w && w->s8_ready && w->d_s8 && w->d_s8_scale; }
+
+kxw4_weight_t w8_of(const tq_qmma_weight_t *w) {
+    kxw4_weight_t d;
+    d.M = w->M;
+    d.K = w->K;
+    d.group = 32;
+    d.scale_enc = KXW4_SCALE_W8;
+    d.codes = w->d_s8;
+    d.scales = w->d_s8_scale;
+    return d;
+}
+
 }  // namespace
 
 extern "C" void kxw4_compat_set_stream(void *stream) { g_stream = static_cast<hipStream_t>(stream); }
@@ -106,6 +119,34 @@ int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode) {
 
 int x_w4_repack_weight(tq_qmma_weight_t *w) { return x_w4_repack_weight_mode(w, 0); }
 
+int x_w8_repack_weight(tq_qmma_weight_t *w) {
+    if (!w || !w->d_A || !w->d_block_scale_inv || !w->block_scaled || !w->e2m3) return -1;
+    if (w->M % 16 || w->K % 128) return -2;
+    uint8_t *codes = nullptr;
+    uint16_t *scales = nullptr;
+    if (hipMalloc(&codes, (size_t)w->M * w->K) != hipSuccess) return KXW4_EHIP;
+    if (hipMalloc(&scales, kxw4_scale_count(w->M, w->K, 32) * sizeof(uint16_t)) != hipSuccess) {
+        dfree(codes);
+        return KXW4_EHIP;
+    }
+    int rc = kxw4_repack_e2m3_s8(w->d_A, w->d_block_scale_inv, w->scale_cols, w->M, w->K, codes, scales,
+                                 g_stream);
+    if (rc == 0 && hipStreamSynchronize(g_stream) != hipSuccess) rc = KXW4_EHIP;
+    if (rc != 0) {
+        dfree(codes);
+        dfree(scales);
+        return rc;
+    }
+    dfree(w->d_A);
+    dfree(w->d_block_scale_inv);
+    w->d_A = nullptr;
+    w->d_block_scale_inv = nullptr;
+    w->d_s8 = codes;
+    w->d_s8_scale = scales;
+    w->s8_ready = 1;
+    return 0;
+}
+
 void x_quantize_act_s8(const float *d_x, int K, int8_t *d_q, float *d_scale, int32_t *d_sum) {
     kxw4_quantize_act(d_x, KXW4_F32, 1, K, 32, d_q, d_scale, d_sum, g_stream);
 }
@@ -128,6 +169,10 @@ void x_rmsnorm_quant(float *d_out, const float *d_in, const uint16_t *d_w, int H
     if (kxw4_rmsnorm_quant(d_out, d_in, d_w, 1, H, eps, 32, g_act.q, g_act.scale, g_act.sum,
                            g_stream) == 0)
         g_act.K = H;
+}
+
+void x_rmsnorm_chunk(float *d_out, const float *d_in, const uint16_t *d_w, int H, int T, float eps) {
+    kxw4_rmsnorm(d_out, d_in, d_w, T, H, eps, g_stream);
 }
 
 int x_gemv_w4a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual) {
@@ -199,15 +244,52 @@ int x_gemm_w4a4(const tq_qmma_weight_t *w, const uint8_t *d_aq4, const float *d_
     return kxw4_gemm_w4a4(&d, d_aq4, d_as4, d_asum4, T, d_y, KXW4_F32, nullptr, g_stream);
 }
 
+int x_gemv_w8a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual) {
+    if (!w8_ready(w) || !d_y) return -1;
+    if (g_act.K != w->K) return -2;
+    const kxw4_weight_t d = w8_of(w);
+    const kxw4_act_t a = prepared_act();
+    return kxw4_gemv(&d, &a, d_y, KXW4_F32, d_residual, 0, g_stream);
+}
+
+int x_gemv_w8a8(const tq_qmma_weight_t *w, const float *d_x, float *d_y) {
+    if (!w || !d_x) return -1;
+    x_prepare_gemv_act_s8(d_x, w->K);
+    return x_gemv_w8a8_prepared(w, d_y, nullptr);
+}
+
+int x_gemv_w8a8_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y) {
+    if (!w || !d_x || !d_residual) return -1;
+    x_prepare_gemv_act_s8(d_x, w->K);
+    return x_gemv_w8a8_prepared(w, d_y, d_residual);
+}
+
+int x_gemm_w8a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as, float *d_y, int T) {
+    if (!w8_ready(w)) return -1;
+    if (!d_aq || !d_as || !d_y || T <= 0 || (T % 8) != 0) return -2;
+    const kxw4_weight_t d = w8_of(w);
+    kxw4_act_t a;
+    a.T = T;
+    a.K = w->K;
+    a.block = 32;
+    a.q = d_aq;
+    a.scale = d_as;
+    a.sum = nullptr;
+    return kxw4_gemm(&d, &a, d_y, KXW4_F32, nullptr, nullptr, 0, 1, g_stream);
+}
+
+// kernels_core.cpp:235-252: W8A8 first, then W4A8.
 int x_gemv_qmma_prepared(const tq_qmma_weight_t *w, const float *d_x, float *d_y,
                          const float *d_residual) {
     if (!w || !d_x || !d_y) return -1;
+    if (w->s8_ready) return x_gemv_w8a8_prepared(w, d_y, d_residual);
     if (w->s4_ready) return x_gemv_w4a8_prepared(w, d_y, d_residual);
     return KXW4_ETIER;
 }
 
 int x_gemv_qmma_add(const tq_qmma_weight_t *w, const float *d_x, const float *d_residual, float *d_y) {
     if (!w || !d_x || !d_residual || !d_y) return -1;
+    if (w->s8_ready) return x_gemv_w8a8_add(w, d_x, d_residual, d_y);
     if (w->s4_ready) return x_gemv_w4a8_add(w, d_x, d_residual, d_y);
     return KXW4_ETIER;
 }

@@ -17,6 +17,10 @@
 // sum = 0 + partial_0 + ... + partial_{S-1}; S == 1 rows store the chain
 // directly (1477-1486).
 //
+// W8 (x_gemm_w8a8, kernels_dpas.cpp:1578-1629): 2 KB int8 weight tiles
+// staged the same way and fed to the K32 MFMA without an unpack; the unit
+// partial carries no factor 16.
+//
 // Block order is XCD-aware: consecutive logical tiles land on one XCD (blocks
 // are dealt round-robin to the 8 XCDs) and are rastered in groups of 4 token
 // tiles so the tiles running together share activation and weight tiles in
@@ -39,12 +43,15 @@ __device__ __forceinline__ int seg_of(const GemmArgs &a, int t) {
     return s;
 }
 
-template <int WM, int UNIT, int MODE, bool SPLITS, bool DEBUG>
+template <int WM, int UNIT, int MODE, bool SPLITS, bool DEBUG, bool W8>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     constexpr int BM = 2 * 16 * WM;
     constexpr int UPS = kTileK / UNIT;
+    static_assert(!W8 || (UNIT == 32 && MODE == 1), "W8: K32 units, reference mode");
+    constexpr int TB = W8 ? 2 : 1;             // 1 KB halves per weight tile
+    constexpr int TILE = kTileBytes * TB;
     __shared__ __attribute__((aligned(16))) uint8_t As[2][BM * kApitch];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][8 * kTileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][8 * TILE];
 
     // ---- block -> (token tile, weight, n-tile) ----
     const int nblk = gridDim.x, id = blockIdx.x;
@@ -75,7 +82,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     // ---- global -> register staging ----
     constexpr int ACH = BM * 8 / kGemmThreads;   // 16-byte activation chunks per thread
     v4i ra[ACH];
-    v4u rb[2];
+    v4u rb[2 * TB];
     auto gload = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < ACH; ++i) {
@@ -87,13 +94,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
             ra[i] = v;
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 2 * TB; ++i) {
             const int c = tid + kGemmThreads * i;
-            const int rgl = c >> 6, l = c & 63;
+            const int rgl = c / (64 * TB), l = c % (64 * TB);
             const int rg = rg0 + rgl;
             v4u v = {0u, 0u, 0u, 0u};
             if (rg < M / 16)
-                v = *reinterpret_cast<const v4u *>(W.codes + ((size_t)rg * NT + kb) * kTileBytes + l * 16);
+                v = *reinterpret_cast<const v4u *>(W.codes + ((size_t)rg * NT + kb) * TILE + l * 16);
             rb[i] = v;
         }
     };
@@ -104,9 +111,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
             *reinterpret_cast<v4i *>(&As[stage][(c >> 3) * kApitch + (c & 7) * 16]) = ra[i];
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 2 * TB; ++i) {
             const int c = tid + kGemmThreads * i;
-            *reinterpret_cast<v4u *>(&Bs[stage][(c >> 6) * kTileBytes + (c & 63) * 16]) = rb[i];
+            *reinterpret_cast<v4u *>(&Bs[stage][(c / (64 * TB)) * TILE + (c % (64 * TB)) * 16]) = rb[i];
         }
     };
 
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
                     }
                     p -= (z[j] * sm) << 4;
                     if (DEBUG && t < T && wrg0 + j < M / 16)
-                        a.dbg[((size_t)t * M + (wrg0 + j) * 16 + n) * Nu + u] = p >> 4;
+                        a.dbg[((size_t)t * M + (wrg0 + j) * 16 + n) * Nu + u] = W8 ? p : p >> 4;
                     if (a.block == 0) f[i][j][r] = __builtin_fmaf((float)p, ws[j], f[i][j][r]);
                     else f[i][j][r] = __builtin_fmaf((float)p, ws[j] * as, f[i][j][r]);
                 }
@@ -221,10 +228,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     };
 
     auto compute = [&](int stage, int kb, const uint16_t (&raw)[UPS][4]) {
-        v4u wd[4];
+        v4u wd[4][TB];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            wd[j] = *reinterpret_cast<const v4u *>(&Bs[stage][(wn * 4 + j) * kTileBytes + lane * 16]);
+#pragma unroll
+            for (int h = 0; h < TB; ++h)
+                wd[j][h] = *reinterpret_cast<const v4u *>(&Bs[stage][(wn * 4 + j) * TILE + h * 1024 + lane * 16]);
         v4i A[WM][2];
 #pragma unroll
         for (int i = 0; i < WM; ++i)
@@ -240,8 +249,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
                 v4i b0[4], b1[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    b0[j] = unpack_k64(wd[j].x, wd[j].y);
-                    b1[j] = unpack_k64(wd[j].z, wd[j].w);
+                    b0[j] = unpack_k64(wd[j][0].x, wd[j][0].y);
+                    b1[j] = unpack_k64(wd[j][0].z, wd[j][0].w);
                 }
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
@@ -255,7 +264,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
                 v4i b[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    b[j] = jj == 0 ? unpack_k64(wd[j].x, wd[j].y) : unpack_k64(wd[j].z, wd[j].w);
+                    b[j] = jj == 0 ? unpack_k64(wd[j][0].x, wd[j][0].y) : unpack_k64(wd[j][0].z, wd[j][0].w);
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -264,8 +273,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
                 long b[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t d = jj == 0 ? wd[j].x : jj == 1 ? wd[j].y : jj == 2 ? wd[j].z : wd[j].w;
-                    b[j] = unpack_k32(d);
+                    if constexpr (W8) {
+                        const v4u h = wd[j][jj >> 1];
+                        b[j] = (jj & 1) ? (long)(((uint64_t)h.w << 32) | h.z) : (long)(((uint64_t)h.y << 32) | h.x);
+                    } else {
+                        const v4u h = wd[j][0];
+                        b[j] = unpack_k32(jj == 0 ? h.x : jj == 1 ? h.y : jj == 2 ? h.z : h.w);
+                    }
                 }
 #pragma unroll
                 for (int i = 0; i < WM; ++i) {
@@ -318,7 +332,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
         for (int r = 0; r < 4; ++r) {
             const int t = tw0 + i * 16 + 4 * g4 + r;
             if (t >= T) continue;
-            const float sc = a.block == 0 ? a.ascale[t] * 0.0625f : 0.0625f;
+            constexpr float kInv16 = W8 ? 1.0f : 0.0625f;   // the nibble unpack's factor 16
+            const float sc = a.block == 0 ? a.ascale[t] * kInv16 : kInv16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int rg = wrg0 + j;
@@ -341,14 +356,22 @@ static void launch_wm_unit(const GemmArgs &a, int mode, bool splits, bool debug,
                            hipStream_t st) {
     const dim3 block(kGemmThreads);
     if (debug) {
-        hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, true>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, true, false>), grid, block, 0, st, a);
     } else if (splits) {
-        if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, true, false>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, false>), grid, block, 0, st, a);
+        if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, true, false, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, false, false>), grid, block, 0, st, a);
     } else {
-        if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, false, false>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, false, false>), grid, block, 0, st, a);
+        if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, false, false, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, false, false, false>), grid, block, 0, st, a);
     }
+}
+
+// W8: K32 units in reference mode, the narrow tile
+static void launch_w8(const GemmArgs &a, bool splits, bool debug, dim3 grid, hipStream_t st) {
+    const dim3 block(kGemmThreads);
+    if (debug) hipLaunchKernelGGL((gemm_kernel<2, 32, 1, true, true, true>), grid, block, 0, st, a);
+    else if (splits) hipLaunchKernelGGL((gemm_kernel<2, 32, 1, true, false, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gemm_kernel<2, 32, 1, false, false, true>), grid, block, 0, st, a);
 }
 
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
@@ -358,11 +381,11 @@ int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
     const char *force = getenv("KXW4_GEMM_KERNEL");
     const bool general = force && strcmp(force, "general") == 0;
     const bool g2 = force && strcmp(force, "gemm2") == 0;
-    if (!debug && !general && !g2) {
+    if (!debug && !general && !g2 && !a.w8) {
         const int r = launch_gemm3(a, st);
         if (r != 1) return r;
     }
-    if (!debug && !general) {
+    if (!debug && !general && !a.w8) {
         const int r = launch_gemm2(a, st);
         if (r != 1) return r;
     }
@@ -382,7 +405,10 @@ int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
     a.t_tiles = (a.T + BM - 1) / BM;
     const dim3 grid(a.n_tiles * a.t_tiles);
     const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
-    if (narrow) {
+    if (a.w8) {
+        if (unit != 32 || mode != 1) return -2;
+        launch_w8(a, splits, debug, grid, st);
+    } else if (narrow) {
         if (unit == 128) launch_wm_unit<2, 128>(a, mode, splits, debug, grid, st);
         else if (unit == 64) launch_wm_unit<2, 64>(a, mode, splits, debug, grid, st);
         else launch_wm_unit<2, 32>(a, mode, splits, debug, grid, st);

@@ -32,6 +32,7 @@ struct DecodeArgs {
     const float *residual;
     int32_t *dbg;
     int T, K, group, block, scale_enc, y_bf16, variant;
+    int w8;                           // int8 weight codes (the W8A8 tier)
     int seg_count;
     int seg_end[kMaxSegments];        // exclusive token end of each segment
     int ts;                           // tokens per work-group slice (set by the launcher)
@@ -60,6 +61,7 @@ struct GemmArgs {
     const float *residual;
     int32_t *dbg;
     int T, K, group, block, scale_enc, y_bf16;
+    int w8;                           // int8 weight codes (the W8A8 tier)
     int seg_count;
     int seg_end[kMaxSegments];        // exclusive token end of each segment
     int n_tiles, t_tiles;             // set by the launcher
@@ -74,10 +76,18 @@ int launch_import_ref(const uint8_t *ref_codes, const uint16_t *ref_scales, int 
 int launch_repack_e2m3(const uint8_t *payload, const float *bs, int scale_cols, int M, int K,
                        int group, uint8_t *out_codes, uint16_t *out_scales, hipStream_t st);
 
+int launch_pack_s8(const int8_t *codes, const uint16_t *scales, int M, int K, uint8_t *out_codes,
+                   uint16_t *out_scales, hipStream_t st);
+int launch_unpack_s8(const uint8_t *codes, const uint16_t *scales, int M, int K, int8_t *out_codes,
+                     uint16_t *out_scales, hipStream_t st);
+int launch_repack_e2m3_s8(const uint8_t *payload, const float *bs, int scale_cols, int M, int K,
+                          uint8_t *out_codes, uint16_t *out_scales, hipStream_t st);
+
 int launch_quantize(const void *x, int x_dtype, int T, int K, int block, int8_t *q,
                     float *scale, int32_t *sum, hipStream_t st);
 int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T, int K,
                           int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
+int launch_rmsnorm(float *out, const float *in, const uint16_t *w, int T, int H, float eps, hipStream_t st);
 int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st);
 

@@ -5,7 +5,8 @@
 // Packed tile (16 rows x 128 K, 1024 bytes): lane l owns bytes [16l, 16l+16),
 // row l%16; dword i of the lane holds k = 32i + 8(l/16) + b with b = 0..3 in
 // the low nibbles of bytes 0..3 and b = 4..7 in the high nibbles, so one
-// 16-byte load per lane feeds two K64 MFMAs (or four K32 MFMAs).
+// 16-byte load per lane feeds two K64 MFMAs (or four K32 MFMAs). The W8A8
+// tier's int8 tiles (2048 bytes) follow the same K slots, below.
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
@@ -207,7 +208,133 @@ __global__ void repack_e2m3_kernel(const uint8_t *__restrict__ payload,
     }
 }
 
+// ---- the W8A8 tier (kernels_dpas.cpp:346-399, 558-575) --------------------
+//
+// W8 tile (16 rows x 128 K, 2048 bytes): half h at byte 1024h; lane l owns
+// bytes [1024h + 16l, +16), row l%16, holding K32 unit j = 2h (bytes 0..7)
+// and j = 2h + 1 (bytes 8..15); byte b of a unit is k = 32j + 8(l/16) + b.
+// So one 16-byte load per lane and half is the operand of two K32 MFMAs,
+// with the same K slots the W4 unpack produces.
+__device__ __forceinline__ DwordCoord dword_coord_s8(int d) {
+    const int h = d >> 8, lane = (d >> 2) & 63, e = d & 3;
+    return {lane & 15, 32 * (2 * h + (e >> 1)) + 8 * (lane >> 4) + 4 * (e & 1)};
+}
+
+__global__ void pack_s8_kernel(const int8_t *__restrict__ codes, int M, int K, uint32_t *__restrict__ out) {
+    const size_t total = (size_t)M * K / 4;
+    const size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= total) return;
+    const int NT = K / kTileK;
+    const size_t tile = d >> 9;
+    const DwordCoord c = dword_coord_s8((int)(d & 511));
+    const int rg = (int)(tile / NT), kb = (int)(tile % NT);
+    const int8_t *src = codes + (size_t)(rg * 16 + c.row) * K + kb * kTileK + c.k0;
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) w |= ((uint32_t)(uint8_t)src[b]) << (8 * b);
+    out[d] = w;
+}
+
+__global__ void unpack_s8_kernel(const uint32_t *__restrict__ in, int M, int K, int8_t *__restrict__ codes) {
+    const size_t total = (size_t)M * K / 4;
+    const size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= total) return;
+    const int NT = K / kTileK;
+    const size_t tile = d >> 9;
+    const DwordCoord c = dword_coord_s8((int)(d & 511));
+    const int rg = (int)(tile / NT), kb = (int)(tile % NT);
+    int8_t *dst = codes + (size_t)(rg * 16 + c.row) * K + kb * kTileK + c.k0;
+    const uint32_t w = in[d];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) dst[b] = (int8_t)(w >> (8 * b));
+}
+
+// w8_repack_kernel's fit with the least-squares sums as fused multiply-adds:
+// s = max(hi/127, neg/128), two refinements, FP16 by round to nearest even.
+__device__ uint16_t fit_int8(const float *wf) {
+    float hi = 0.0f, neg = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        hi = fmaxf(hi, wf[j]);
+        neg = fmaxf(neg, -wf[j]);
+    }
+    float s = fmaxf(hi / 127.0f, neg / 128.0f);
+    if (!(s > 0.0f)) s = 1.0f;
+    for (int iter = 0; iter < 2; ++iter) {
+        float num = 0.0f, den = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float q = clampf(rintf(wf[j] / s), -128.0f, 127.0f);
+            num = __builtin_fmaf(wf[j], q, num);
+            den = __builtin_fmaf(q, q, den);
+        }
+        if (den > 0.0f) s = num / den;
+    }
+    return __builtin_bit_cast(uint16_t, (_Float16)s);
+}
+
+// One thread per (row, K32): decode, fit, write the unit's 8 dwords (two per
+// lane group) and its tiled FP16 scale.
+__global__ void repack_e2m3_s8_kernel(const uint8_t *__restrict__ payload, const float *__restrict__ bs,
+                                      int scale_cols, int M, int K, uint32_t *__restrict__ out_codes,
+                                      uint16_t *__restrict__ out_scales) {
+    const int Kt = K / 32, NT = K / kTileK;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)M * Kt) return;
+    const int row = (int)(i / Kt), kt = (int)(i % Kt);
+    const int mt = row >> 4, n = row & 15;
+    const int sc = (scale_cols == Kt) ? kt : (kt >> 2);
+    const float b = bs[(size_t)(mt >> 3) * scale_cols + sc];
+    float wf[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) wf[j] = e2m3f(e2m3_code_at(payload, Kt, row, kt * 32 + j)) * b;
+    const uint16_t sh = fit_int8(wf);
+    out_scales[((size_t)mt * Kt + kt) * 16 + n] = sh;
+    const float st = half_bits_to_float(sh);
+    const int kb = kt >> 2, j = kt & 3;
+    uint32_t *tile = out_codes + ((size_t)mt * NT + kb) * 512 + 256 * (j >> 1);
+#pragma unroll
+    for (int gl = 0; gl < 4; ++gl)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const int q = (int)clampf(rintf(wf[8 * gl + 4 * e + bb] / st), -128.0f, 127.0f);
+                w |= (uint32_t)(uint8_t)q << (8 * bb);
+            }
+            tile[(n + 16 * gl) * 4 + 2 * (j & 1) + e] = w;
+        }
+}
+
 static inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+int launch_pack_s8(const int8_t *codes, const uint16_t *scales, int M, int K, uint8_t *out_codes,
+                   uint16_t *out_scales, hipStream_t st) {
+    const size_t nd = (size_t)M * K / 4, ns = (size_t)M * (K / 32);
+    hipLaunchKernelGGL(pack_s8_kernel, dim3(blocks_for(nd, 256)), dim3(256), 0, st, codes, M, K,
+                       reinterpret_cast<uint32_t *>(out_codes));
+    hipLaunchKernelGGL(scales_to_tiled_kernel, dim3(blocks_for(ns, 256)), dim3(256), 0, st, scales, M,
+                       K / 32, out_scales);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int launch_unpack_s8(const uint8_t *codes, const uint16_t *scales, int M, int K, int8_t *out_codes,
+                     uint16_t *out_scales, hipStream_t st) {
+    const size_t nd = (size_t)M * K / 4, ns = (size_t)M * (K / 32);
+    hipLaunchKernelGGL(unpack_s8_kernel, dim3(blocks_for(nd, 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint32_t *>(codes), M, K, out_codes);
+    if (out_scales)
+        hipLaunchKernelGGL(scales_to_natural_kernel, dim3(blocks_for(ns, 256)), dim3(256), 0, st, scales,
+                           M, K / 32, out_scales);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int launch_repack_e2m3_s8(const uint8_t *payload, const float *bs, int scale_cols, int M, int K,
+                          uint8_t *out_codes, uint16_t *out_scales, hipStream_t st) {
+    const size_t n = (size_t)M * (K / 32);
+    hipLaunchKernelGGL(repack_e2m3_s8_kernel, dim3(blocks_for(n, 128)), dim3(128), 0, st, payload, bs,
+                       scale_cols, M, K, reinterpret_cast<uint32_t *>(out_codes), out_scales);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
 
 int launch_pack(const int8_t *codes, const uint16_t *scales, int M, int K, int group,
                 uint8_t *out_codes, uint16_t *out_scales, hipStream_t st) {

@@ -315,6 +315,27 @@ int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T,
     return launch_q<kSiluMul>(a, block, st);
 }
 
+// x_rmsnorm_chunk (kernels_dpas.cpp:1124-1144): the (1+w) RMSNorm of
+// x_rmsnorm_quant over T rows without the quantizer; the sum of squares and
+// the scaling are the quantizer's own (same partial sums, same reduction), so
+// both entry points write identical rows.
+__global__ __launch_bounds__(kQThreads) void rmsnorm_kernel(QuantArgs a) {
+    __shared__ float red[kQThreads / 64];
+    const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
+    const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
+    float ss = 0.0f;
+    for (int k = tid; k < K; k += kQThreads) ss += row[k] * row[k];
+    ss = block_reduce_sum(ss, red);
+    const float rms_inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+    for (int k = tid; k < K; k += kQThreads) a.out[(size_t)t * K + k] = produce<kRmsNorm>(a, t, k, rms_inv);
+}
+
+int launch_rmsnorm(float *out, const float *in, const uint16_t *w, int T, int H, float eps, hipStream_t st) {
+    QuantArgs a{in, nullptr, w, out, nullptr, nullptr, nullptr, T, H, eps};
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kQThreads), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
 int launch_rmsnorm_quant(float *out, const float *in, const uint16_t *w, int T, int H, float eps,
                          int block, int8_t *q, float *scale, int32_t *sum, hipStream_t st) {
     QuantArgs a{in, nullptr, w, out, q, scale, sum, T, H, eps};

@@ -19,6 +19,12 @@
 // loop is a per-ring base plus an immediate offset. Whole rings run without
 // predicates; only a split's last, partial ring selects the old accumulator
 // for its padded positions.
+//
+// W8 (the W8A8 tier, x_gemv_w8a8_core / x_gemm_w8a8, kernels_dpas.cpp:
+// 771-844, 1578-1629): 2 KB int8 tiles, two 16-byte loads per lane and tile,
+// used as the K32 MFMA operand without an unpack; the MFMA result is the unit
+// partial itself (no factor 16) and the chain is the reference mode's with
+// zero point 0.
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
@@ -31,9 +37,12 @@ constexpr int kRwWaves = 8;                 // waves per work-group by default
 constexpr int kRwMaxWaves = 16;
 constexpr size_t kRwLdsMax = 160 * 1024;
 
-template <int TT, int UNIT, int MODE, bool ALT2, int PF>
+template <int TT, int UNIT, int MODE, bool ALT2, int PF, bool W8>
 __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeArgs a) {
     constexpr int UPS = kTileK / UNIT;
+    static_assert(!W8 || (UNIT == 32 && MODE == 1), "W8: K32 units, reference mode");
+    constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
+    constexpr float kInv16 = W8 ? 1.0f : 0.0625f;  // undoes the nibble unpack's factor 16
     static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -101,17 +110,21 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     const int ls = __builtin_ctz(S);
     int u0 = (Nu * sb) >> ls, u1 = (Nu * (sb + 1)) >> ls;
     int kt0 = u0 / UPS, ntw = (u1 + UPS - 1) / UPS - kt0;
-    const v4u *wrow = reinterpret_cast<const v4u *>(W.codes + (size_t)rg * NT * kTileBytes) + lane;
-    v4u ring[PF];
+    const v4u *wrow = reinterpret_cast<const v4u *>(W.codes + (size_t)rg * NT * kTileBytes * TB) + lane;
+    v4u ring[PF][TB];
     // tile i of the current split; an empty split (more splits than units)
     // or an idle wave reads a valid tile it never uses
-    auto load = [&](int i) { return wrow[(size_t)min(kt0 + max(i, 0), NT - 1) * (kTileBytes / 16)]; };
+    auto load = [&](int i, v4u (&dst)[TB]) {
+        const size_t t = (size_t)min(kt0 + max(i, 0), NT - 1) * (kTileBytes * TB / 16);
+#pragma unroll
+        for (int h = 0; h < TB; ++h) dst[h] = wrow[t + 64 * h];
+    };
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < PF; ++p) ring[p] = load(min(p, ntw - 1));
+    for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), ring[p]);
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
-    __builtin_amdgcn_s_waitcnt(0x0F70 | PF);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * TB));
     const bool ref_block = a.block == 32, zp = a.scale_enc == 1;
     if (MODE != 0) {
         // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
@@ -145,7 +158,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                 kt0 = u0 / UPS;
                 ntw = (u1 + UPS - 1) / UPS - kt0;
 #pragma unroll
-                for (int p = 0; p < PF; ++p) ring[p] = load(min(p, ntw - 1));
+                for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), ring[p]);
             }
             float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -162,7 +175,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                     const int kb = kt0 + i;
                     const v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
                     const v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
-                    const v4u wd = ring[p];
+                    const v4u wd = ring[p][0];
 #pragma unroll
                     for (int j = 0; j < UPS; ++j) {
                         const int u = kb * UPS + j;
@@ -176,11 +189,18 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                             acc = j == 0 ? mfma_k64(A0, unpack_k64(wd.x, wd.y), zero)
                                          : mfma_k64(A1, unpack_k64(wd.z, wd.w), zero);
                         } else {
-                            const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
                             const v4i c = j < 2 ? A0 : A1;
                             const long av = (j & 1) ? (long)(((uint64_t)(uint32_t)c.w << 32) | (uint32_t)c.z)
                                                     : (long)(((uint64_t)(uint32_t)c.y << 32) | (uint32_t)c.x);
-                            acc = mfma_k32(av, unpack_k32(d), zero);
+                            long bv;
+                            if constexpr (W8) {
+                                const v4u h = ring[p][j >> 1];
+                                bv = (j & 1) ? (long)(((uint64_t)h.w << 32) | h.z)
+                                             : (long)(((uint64_t)h.y << 32) | h.x);
+                            } else {
+                                bv = unpack_k32(j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w);
+                            }
+                            acc = mfma_k32(av, bv, zero);
                         }
                         // MODE 0 has unit == group, so unit u reads scale u
                         const uint16_t *sp = MODE == 0 ? &sr[(p * UPS + j) * 16] : &sbase[(u >> gsh) * 16];
@@ -217,7 +237,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                             }
                         }
                     }
-                    ring[p] = load(min(i + PF, ntw - 1));
+                    load(min(i + PF, ntw - 1), ring[p]);
                     // keep each slot's unpack behind the previous slot's load, so
                     // the wait before it covers only that slot
                     __builtin_amdgcn_sched_barrier(0);
@@ -259,7 +279,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     for (int r = 0; r < 4; ++r) {
         const int t = 4 * g4 + r;
         if (t >= T) continue;
-        const float v = a.block == 0 ? res[r] * (a.ascale[t] * 0.0625f) : res[r] * 0.0625f;
+        const float v = a.block == 0 ? res[r] * (a.ascale[t] * kInv16) : res[r] * kInv16;
         float out;
         if (a.residual) out = v + a.residual[(size_t)t * M + row];
         else if (ALT2 && S > 1) out = v + 0.0f;
@@ -269,9 +289,9 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     }
 }
 
-template <int TT, int UNIT, int MODE, bool ALT2, int PF>
+template <int TT, int UNIT, int MODE, bool ALT2, int PF, bool W8 = false>
 static int rw_launch(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-    auto k = rowwave_kernel<TT, UNIT, MODE, ALT2, PF>;
+    auto k = rowwave_kernel<TT, UNIT, MODE, ALT2, PF, W8>;
     static bool attr = false;
     if (!attr) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -375,6 +395,15 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // flight at the start delay the staging)
     const char *pfe = getenv("KXW4_ROWWAVE_PF");
     const bool pf8 = pfe && atoi(pfe) == 8 && tiles >= 16;
+    if (a.w8) {
+        if (unit != 32 || mode != 1) return 1;
+        const bool alt2 = a.variant == kVarGemv;
+        if (a.T <= 8)
+            return alt2 ? rw_launch<8, 32, 1, true, 4, true>(a, grid, block, lds, st)
+                        : rw_launch<8, 32, 1, false, 4, true>(a, grid, block, lds, st);
+        return alt2 ? rw_launch<16, 32, 1, true, 4, true>(a, grid, block, lds, st)
+                    : rw_launch<16, 32, 1, false, 4, true>(a, grid, block, lds, st);
+    }
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, block, lds, st);
     return rw_unit<16>(a, unit, mode, pf8, grid, block, lds, st);
 }

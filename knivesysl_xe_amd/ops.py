@@ -6,11 +6,13 @@ of the reference's library-global scratch:
 
     reference                         here
     x_w4_repack_weight_mode           W4Weight.repack_e2m3
+    x_w8_repack_weight                W4Weight.repack_e2m3_s8 (W8A8 tier)
     (load-time integer codes)         W4Weight.from_codes
     reference DPAS layout import      W4Weight.from_reference_layout
     x_quantize_act_s8 / _chunk        quantize_act
     x_silu_mul_quant                  silu_mul_quant
     x_rmsnorm_quant (+ chunk)         rmsnorm_quant
+    x_rmsnorm_chunk                   rmsnorm
     x_gemv_w4a8[_add|_prepared]       gemv
     x_gemv_w4a8_fanout                gemv_fanout
     x_gemm_w4a8                       gemm
@@ -31,7 +33,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import BF16, F32, SCALE_FP16, SCALE_FP16_ZP4, check, lib
+from ._lib import BF16, F32, SCALE_FP16, SCALE_FP16_ZP4, SCALE_W8, check, lib
 
 
 def _stream():
@@ -73,7 +75,8 @@ class W4Weight:
 
     @classmethod
     def empty(cls, M: int, K: int, group: int, scale_enc: int, device="cuda") -> "W4Weight":
-        codes = torch.empty(M * K // 2, dtype=torch.uint8, device=device)
+        nbytes = M * K if scale_enc == SCALE_W8 else M * K // 2
+        codes = torch.empty(nbytes, dtype=torch.uint8, device=device)
         scales = torch.empty(M * (K // group), dtype=torch.int16, device=device)
         return cls(M, K, group, scale_enc, codes, scales)
 
@@ -85,6 +88,25 @@ class W4Weight:
         w = cls.empty(M, K, group, scale_enc, codes.device)
         check("kxw4_pack_weight", lib().kxw4_pack_weight(
             _ptr(codes), _ptr(scales), M, K, group, _ptr(w.codes), _ptr(w.scales), _stream()))
+        return w
+
+    @classmethod
+    def from_codes_s8(cls, codes: torch.Tensor, scales: torch.Tensor) -> "W4Weight":
+        """W8A8 tier: codes int8 [M][K]; scales int16 (FP16 bits) [M][K/32]."""
+        M, K = codes.shape
+        w = cls.empty(M, K, 32, SCALE_W8, codes.device)
+        check("kxw4_pack_weight_s8", lib().kxw4_pack_weight_s8(
+            _ptr(codes), _ptr(scales), M, K, _ptr(w.codes), _ptr(w.scales), _stream()))
+        return w
+
+    @classmethod
+    def repack_e2m3_s8(cls, payload: torch.Tensor, block_scale_inv: torch.Tensor, scale_cols: int,
+                       M: int, K: int) -> "W4Weight":
+        """x_w8_repack_weight: dense-E2M3 payload -> the W8A8 tier."""
+        w = cls.empty(M, K, 32, SCALE_W8, payload.device)
+        check("kxw4_repack_e2m3_s8", lib().kxw4_repack_e2m3_s8(
+            _ptr(payload), _ptr(block_scale_inv), scale_cols, M, K, _ptr(w.codes), _ptr(w.scales),
+            _stream()))
         return w
 
     @classmethod
@@ -235,6 +257,15 @@ def rmsnorm_quant(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, block:
         _ptr(out), _ptr(x), _ptr(w_bf16_bits), T, H, eps, block, _ptr(a.q), _ptr(a.scale),
         _ptr(a.sum), _stream()))
     return out, a
+
+
+def rmsnorm(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, out=None) -> torch.Tensor:
+    """Batched (1+w) RMSNorm of [T][H] f32 rows (x_rmsnorm_chunk)."""
+    T, H = x.shape
+    y = out if out is not None else torch.empty(T, H, dtype=torch.float32, device=x.device)
+    check("kxw4_rmsnorm", lib().kxw4_rmsnorm(_ptr(y), _ptr(x), _ptr(w_bf16_bits), T, H, eps,
+                                             _stream()))
+    return y
 
 
 def _out(T: int, M: int, dtype, device, out=None):

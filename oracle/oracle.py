@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(HERE, "_build", "libw4a8_oracle.so")
 
 SCALE_FP16 = 0
 SCALE_FP16_ZP4 = 1
+SCALE_S8 = 2
 VAR_GEMV = 0
 VAR_FANOUT = 1
 VAR_GEMM = 2
@@ -73,6 +74,8 @@ def lib():
             "orc_rmsnorm": (None, [P, P, C.c_int, C.c_float, P]),
             "orc_fit_int4_asym": (C.c_uint16, [P, C.c_int, C.c_int, C.c_int, P]),
             "orc_repack_e2m3": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, P]),
+            "orc_fit_int8": (C.c_uint16, [P, C.c_int, C.c_int]),
+            "orc_repack_e2m3_s8": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P]),
             "orc_pack_ref_layout": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P]),
             "orc_unpack_ref_layout": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P]),
             "orc_gemv_splits": (C.c_int, [C.c_int]),
@@ -189,6 +192,25 @@ def repack_e2m3(payload, block_scale_inv, scale_cols: int, M: int, K: int, mode:
                                _ptr(codes), _ptr(scales))
     if rc:
         raise ValueError(f"orc_repack_e2m3 rc={rc}")
+    return codes, scales
+
+
+def fit_int8(wf, contract: bool = True) -> int:
+    wf = _c(wf, np.float32)
+    return int(lib().orc_fit_int8(_ptr(wf), wf.size, int(contract)))
+
+
+def repack_e2m3_s8(payload, block_scale_inv, scale_cols: int, M: int, K: int,
+                   contract: bool = True):
+    """W8A8 tier: int8 codes [M][K] and plain FP16 scales [M][K/32]."""
+    payload = _c(payload, np.uint8)
+    bs = _c(block_scale_inv, np.float32)
+    codes = np.empty((M, K), np.int8)
+    scales = np.empty((M, K // 32), np.uint16)
+    rc = lib().orc_repack_e2m3_s8(_ptr(payload), _ptr(bs), scale_cols, M, K, int(contract),
+                                  _ptr(codes), _ptr(scales))
+    if rc:
+        raise ValueError(f"orc_repack_e2m3_s8 rc={rc}")
     return codes, scales
 
 

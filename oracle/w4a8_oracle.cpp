@@ -190,6 +190,35 @@ int orc_quantize_act_s4(const float *x, int T, int K, int8_t *q, float *scale, i
     return 0;
 }
 
+// w8_repack_kernel's fit (kernels_dpas.cpp:346-399): s = max(hi/127, neg/128)
+// (1 when not positive), two least-squares refinements s = sum(w q)/sum(q q)
+// with q = clamp(rint(w/s), -128, 127), then the FP16 (round to nearest even)
+// of s; no zero point, no reserved nibble.
+uint16_t orc_fit_int8(const float *wf, int n, int contract) {
+    float hi = 0.0f, neg = 0.0f;
+    for (int j = 0; j < n; ++j) {
+        hi = std::fmax(hi, wf[j]);
+        neg = std::fmax(neg, -wf[j]);
+    }
+    float s = std::fmax(hi / 127.0f, neg / 128.0f);
+    if (!(s > 0.0f)) s = 1.0f;
+    for (int iter = 0; iter < 2; ++iter) {
+        float num = 0.0f, den = 0.0f;
+        for (int j = 0; j < n; ++j) {
+            const float q = clampf(std::rint(wf[j] / s), -128.0f, 127.0f);
+            if (contract) {
+                num = std::fma(wf[j], q, num);
+                den = std::fma(q, q, den);
+            } else {
+                num = num + wf[j] * q;
+                den = den + q * q;
+            }
+        }
+        if (den > 0.0f) s = num / den;
+    }
+    return orc_f32_to_f16(s);
+}
+
 // kernels_dpas.cpp:197-199 (quantize_act_s8<true>): v = (g/(1+exp(-g)))*u.
 void orc_silu_mul(const float *gate, const float *up, float *out, int n) {
     for (int i = 0; i < n; ++i) {
@@ -288,6 +317,32 @@ int orc_repack_e2m3(const uint8_t *payload, const float *bs, int scale_cols, int
 // 62-72): codes [M/16][Kt][256 B]; row n of a row-group owns bytes
 // [16n, 16n+16) of a tile; dword i holds k = 8i..8i+7; byte b holds k = 8i+2b
 // (low nibble) and 8i+2b+1 (high). Scales [M/16][K/group][16], row fastest.
+// x_w8_repack_weight (kernels_dpas.cpp:346-399, 558-575): dense-E2M3 payload ->
+// int8 codes [M][K] and plain FP16 scales [M][K/32], per (row, K32).
+int orc_repack_e2m3_s8(const uint8_t *payload, const float *bs, int scale_cols, int M, int K,
+                       int contract, int8_t *codes, uint16_t *scales) {
+    if (!payload || !bs || !codes || !scales) return -1;
+    if (M % 16 || K % 128) return -2;
+    const int Kt = K / 32;
+    for (int row = 0; row < M; ++row) {
+        const int mt = row >> 4;
+        for (int kt = 0; kt < Kt; ++kt) {
+            const int sc = (scale_cols == Kt) ? kt : (kt >> 2);
+            const float b = bs[(size_t)(mt >> 3) * scale_cols + sc];
+            float wf[32];
+            for (int j = 0; j < 32; ++j)
+                wf[j] = orc_e2m3(orc_e2m3_code_at(payload, Kt, row, kt * 32 + j)) * b;
+            const uint16_t sh = orc_fit_int8(wf, 32, contract);
+            scales[(size_t)row * Kt + kt] = sh;
+            const float st = orc_f16_to_f32(sh);
+            for (int j = 0; j < 32; ++j)
+                codes[(size_t)row * K + kt * 32 + j] =
+                    (int8_t)(int)clampf(std::rint(wf[j] / st), -128.0f, 127.0f);
+        }
+    }
+    return 0;
+}
+
 int orc_pack_ref_layout(const int8_t *codes, const uint16_t *scales, int M, int K,
                         int group, uint8_t *ref_codes, uint16_t *ref_scales) {
     if (M % 16 || K % 32 || (group != 32 && group != 64)) return -2;
@@ -400,7 +455,12 @@ static int check_args(const orc_weight_t *w, const orc_act_t *a) {
     // K64-tier weights with FP16|zp scales only
     if (a->block == 64 && (w->group != 64 || w->scale_enc != ORC_SCALE_FP16_ZP4)) return -1;
     if (w->scale_enc == ORC_SCALE_FP16_ZP4 && !a->sum) return -1;
-    if (w->scale_enc != ORC_SCALE_FP16 && w->scale_enc != ORC_SCALE_FP16_ZP4) return -2;
+    // the W8A8 tier (kernels_dpas.cpp:771-844, 1578-1629): int8 codes, plain
+    // FP16 scales per K32, block-32 activations only
+    if (w->scale_enc == ORC_SCALE_S8 && (w->group != 32 || a->block != 32)) return -1;
+    if (w->scale_enc != ORC_SCALE_FP16 && w->scale_enc != ORC_SCALE_FP16_ZP4 &&
+        w->scale_enc != ORC_SCALE_S8)
+        return -2;
     return 0;
 }
 

@@ -16,6 +16,10 @@
  *                    point in its low nibble (ORC_SCALE_FP16_ZP4).
  *   config mode    : per-token activation scale (block 0), weight group 64 or
  *                    128, plain FP16 scale, zero point 0 (ORC_SCALE_FP16).
+ *   W8A8 mode      : int8 weight codes with plain FP16 scales per K32
+ *                    (ORC_SCALE_S8) and block-32 activations: the reference
+ *                    mode arithmetic with zero point 0 (kernels_dpas.cpp:
+ *                    771-844 GEMV, 1578-1629 GEMM).
  *   W4A4 mode      : s4 activations (block 64: codes in [-7, 7], one FP32
  *                    scale and one code sum per (token, K64)), K64 weights
  *                    with FP16|zp scales, the GEMM variant (x_gemm_w4a4,
@@ -41,6 +45,10 @@
  *                    (row, col) owns a distinct contiguous 6-bit field of its
  *                    384-byte tile; the bit positions themselves restate
  *                    kernels_core.cpp:46-75 and no reference vector checks them
+ *   orc_fit_int8     known answers (exactly representable groups reproduce
+ *                    their step, clamp asymmetry at -128/127) and invariants;
+ *                    the refinement's rounding on general inputs restates
+ *                    kernels_dpas.cpp:363-377 (parity unpinned beyond those)
  *   orc_fit_int4_asym parity unpinned beyond known answers and invariants
  *                    (exact fits of evenly spaced groups, zero kept, nibble
  *                    reserved, codes within half a step); the least-squares
@@ -64,7 +72,9 @@
 extern "C" {
 #endif
 
-enum { ORC_SCALE_FP16 = 0, ORC_SCALE_FP16_ZP4 = 1 };
+/* ORC_SCALE_S8: the W8A8 tier, int8 codes in [-128, 127] with plain FP16
+ * scales per (row, K32) */
+enum { ORC_SCALE_FP16 = 0, ORC_SCALE_FP16_ZP4 = 1, ORC_SCALE_S8 = 2 };
 enum { ORC_VAR_GEMV = 0, ORC_VAR_FANOUT = 1, ORC_VAR_GEMM = 2 };
 
 /* ---- scalar conversions ---------------------------------------------- */
@@ -101,6 +111,12 @@ uint16_t orc_fit_int4_asym(const float *wf, int n, int reserve_nibble,
 int orc_repack_e2m3(const uint8_t *payload, const float *block_scale_inv,
                     int scale_cols, int M, int K, int mode, int contract,
                     int8_t *codes, uint16_t *scales);
+/* W8A8 tier: the int8 fit of w8_repack_kernel and the E2M3 -> int8 repack
+ * (natural codes [M][K], FP16 scales [M][K/32]). */
+uint16_t orc_fit_int8(const float *wf, int n, int contract);
+int orc_repack_e2m3_s8(const uint8_t *payload, const float *block_scale_inv,
+                       int scale_cols, int M, int K, int contract,
+                       int8_t *codes, uint16_t *scales);
 /* natural codes/scales <-> the reference's lane-major K32 DPAS layout */
 int orc_pack_ref_layout(const int8_t *codes, const uint16_t *scales, int M,
                         int K, int group, uint8_t *ref_codes,

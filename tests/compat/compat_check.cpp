@@ -185,6 +185,13 @@ int main() {
     std::vector<float> xn(2048);
     orc_rmsnorm(x.data(), wn.data(), 2048, 1e-6f, xn.data());
     check(same_bits(host_copy(dnorm, 2048), xn), "x_rmsnorm_quant hidden == oracle");
+    {
+        float *dn2;
+        HIPCHECK(hipMalloc(&dn2, 2048 * sizeof(float)));
+        x_rmsnorm_chunk(dn2, dx, dwn, 2048, 1, 1e-6f);
+        check(same_bits(host_copy(dn2, 2048), xn), "x_rmsnorm_chunk == oracle");
+        HIPCHECK(hipFree(dn2));
+    }
     const std::vector<int> sp64(1, orc_gemv_splits(512 / 16));
     check(x_gemv_w4a8_prepared(&w64, dy) == 0 &&
               same_bits(host_copy(dy, 512), oracle_project(s64, xn, 1, ORC_VAR_GEMV, sp64, nullptr)),
@@ -285,6 +292,50 @@ int main() {
         HIPCHECK(hipFree(das4));
         HIPCHECK(hipFree(dsum4));
         HIPCHECK(hipFree(dy4));
+    }
+
+    // ---- W8A8 tier: x_w8_repack_weight, GEMV (+add, tier routing), GEMM ---
+    {
+        const int M8 = 512, K8 = 2048;
+        Source s8 = make_source(rng, M8, K8, 0);
+        tq_qmma_weight_t w8 = make_weight(s8);
+        check(x_w8_repack_weight(&w8) == 0 && w8.s8_ready && !w8.d_A && w8.d_s8, "x_w8_repack_weight");
+        std::vector<int8_t> c8((size_t)M8 * K8);
+        std::vector<uint16_t> sc8((size_t)M8 * (K8 / 32));
+        orc_repack_e2m3_s8(s8.payload.data(), s8.bs.data(), s8.scale_cols, M8, K8, 1, c8.data(), sc8.data());
+        orc_weight_t o8{M8, K8, 32, ORC_SCALE_S8, c8.data(), sc8.data()};
+        auto proj8 = [&](const std::vector<float> &xv, int T, int variant, const std::vector<int> &sp,
+                         const float *resid) {
+            std::vector<int8_t> q((size_t)T * K8);
+            std::vector<float> sc((size_t)T * (K8 / 32));
+            std::vector<int32_t> sm((size_t)T * (K8 / 32));
+            orc_quantize_act(xv.data(), T, K8, 32, q.data(), sc.data(), sm.data());
+            orc_act_t a{T, K8, 32, q.data(), sc.data(), sm.data()};
+            std::vector<float> y((size_t)T * M8, 0.0f);
+            orc_project(&o8, &a, variant, sp.data(), 1, resid, 0, y.data(), 0, M8);
+            return y;
+        };
+        const std::vector<int> sp8(1, orc_gemv_splits(M8 / 16));
+        check(x_gemv_w8a8(&w8, dx, dy) == 0 && same_bits(host_copy(dy, M8), proj8(x, 1, ORC_VAR_GEMV, sp8, nullptr)),
+              "x_gemv_w8a8 == oracle");
+        check(x_gemv_w8a8_add(&w8, dx, dres, dy) == 0 &&
+                  same_bits(host_copy(dy, M8), proj8(x, 1, ORC_VAR_GEMV, sp8, res.data())),
+              "x_gemv_w8a8_add == oracle");
+        check(x_gemv_qmma_prepared(&w8, dx, dy, dres) == 0 &&
+                  same_bits(host_copy(dy, M8), proj8(x, 1, ORC_VAR_GEMV, sp8, res.data())),
+              "x_gemv_qmma_prepared routes to W8A8");
+        const std::vector<int> one(T, 1);
+        check(x_gemm_w8a8(&w8, daq, das, dyt, T) == 0 &&
+                  same_bits(host_copy(dyt, (size_t)T * M8), proj8(xt, T, ORC_VAR_GEMM, one, nullptr)),
+              "x_gemm_w8a8 (T = 72) == oracle");
+        const std::vector<int> one8(8, 1);
+        const std::vector<float> x8(xt.begin(), xt.begin() + (size_t)8 * K8);
+        check(x_gemm_w8a8(&w8, daq, das, dyt, 8) == 0 &&
+                  same_bits(host_copy(dyt, (size_t)8 * M8), proj8(x8, 8, ORC_VAR_GEMM, one8, nullptr)),
+              "x_gemm_w8a8 (T = 8, spec wave) == oracle");
+        check(x_gemm_w8a8(&w8, daq, das, dyt, 36) == -2, "x_gemm_w8a8 T % 8 != 0 = -2");
+        check(x_gemm_w8a8(&w32, daq, das, dyt, 8) == -1, "x_gemm_w8a8 without s8 = -1");
+        check(x_gemv_w8a8(&w32, dx, dy) == -1, "x_gemv_w8a8 without s8 = -1");
     }
 
     // ---- argument checks keep the reference's codes ------------------------

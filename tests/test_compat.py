@@ -44,6 +44,8 @@ def test_library_exports_reference_signatures():
     assert exported["x_gemm_w4a4"] == ("tq_qmma_weight_t const*, unsigned char const*, float const*, "
                                        "int const*, float*, int")
     assert exported["x_quantize_act_chunk_s4"] == "float const*, int, int, unsigned char*, float*, int*"
+    assert exported["x_gemm_w8a8"] == "tq_qmma_weight_t const*, signed char const*, float const*, float*, int"
+    assert exported["x_rmsnorm_chunk"] == "float*, float const*, unsigned short const*, int, int, float"
     assert "kxw4_compat_set_stream" in out
 
 

@@ -187,6 +187,22 @@ def test_rmsnorm_quant(block):
     assert np.array_equal(a.sum.cpu().numpy(), sm)
 
 
+@pytest.mark.parametrize("T,H", [(1, 2048), (5, 5120), (300, 640), (2, 1000)])
+def test_rmsnorm_chunk(T, H):
+    # x_rmsnorm_chunk (kernels_dpas.cpp:1124-1144): the rows kxw4_rmsnorm_quant
+    # writes, bit for bit, and the oracle's norm within 2e-6
+    rng = np.random.default_rng(T + H)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = O.f32_to_bf16(rng.standard_normal(H).astype(np.float32) * 0.1)
+    y = ops.rmsnorm(dev(x), dev(w.view(np.int16)), 1e-6).cpu().numpy()
+    for t in range(T):
+        ref = O.rmsnorm(x[t], w, 1e-6)
+        assert np.max(np.abs(y[t] - ref)) <= 2e-6 * np.max(np.abs(ref))
+    if H % 64 == 0:
+        normed, _ = ops.rmsnorm_quant(dev(x), dev(w.view(np.int16)), 1e-6, 32)
+        assert np.array_equal(normed.cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+
 # ------------------------------------------------------------------ partials
 @pytest.mark.parametrize("name", ["ref32", "ref64", "cfg128", "cfg64"])
 def test_partials_golden(golden, name):

@@ -488,3 +488,89 @@ def test_w4a4_rejects_other_tiers_and_variants():
         O.project(codes, scales[:, ::2].copy(), 128, 1, q, s, sm, 64, O.VAR_GEMM, 1)
     with pytest.raises(ValueError, match="rc=-1"):
         O.project(codes, scales & 0xFFF0, 64, 0, q, s, sm, 64, O.VAR_GEMM, 1)
+
+
+# ---- W8A8 tier: int8 fit and projection -------------------------------------
+
+def test_fit_int8_known_answers():
+    # w8_repack_kernel (kernels_dpas.cpp:346-399): a group on an exact grid of
+    # step 1/16 keeps that step through both refinements
+    wf = (0.5 * (np.arange(32) - 16)).astype(np.float32)
+    assert O.fit_int8(wf) == 0x2C00                              # fp16(0.0625)
+    # the negative side divides by 128: a lone -1 with grid-aligned positives
+    # gives s = 1/128 and code -128 (the positive side's 127 would not reach)
+    wf = (np.arange(32) % 5 / 128.0).astype(np.float32)
+    wf[7] = -1.0
+    assert O.fit_int8(wf) == 0x2000                              # fp16(1/128)
+    assert O.fit_int8(np.zeros(32, np.float32)) == 0x3C00        # scale 1
+
+
+def test_fit_int8_invariants():
+    rng = np.random.default_rng(31)
+    for _ in range(200):
+        wf = (rng.standard_normal(32) * np.exp2(rng.integers(-12, 4))).astype(np.float32)
+        sh = O.fit_int8(wf)
+        st = np.float32(np.uint16(sh).view(np.float16))
+        assert st > 0
+        q = np.clip(np.rint(wf / st), -128, 127)
+        inside = (q > -128) & (q < 127)
+        assert np.all(np.abs(wf[inside] - q[inside] * st) <= 0.5 * st * (1 + 1e-6))
+        # the fit lands within a few percent of the absmax step
+        s0 = max(wf.max() / 127, -wf.min() / 128)
+        assert 0.9 * s0 <= st <= 1.1 * s0
+
+
+def test_repack_e2m3_s8_uses_the_fit_per_k32():
+    rng = np.random.default_rng(32)
+    M, K = 32, 256
+    payload, bs, scale_cols = random_payload(rng, M, K)
+    codes, scales = O.repack_e2m3_s8(payload, bs, scale_cols, M, K)
+    wf = decode_payload(payload, bs, scale_cols, M, K)
+    for row in (0, 17, 31):
+        for kt in range(K // 32):
+            g = wf[row, kt * 32:(kt + 1) * 32]
+            assert scales[row, kt] == O.fit_int8(g)
+            st = np.float32(np.uint16(scales[row, kt]).view(np.float16))
+            assert np.array_equal(codes[row, kt * 32:(kt + 1) * 32],
+                                  np.clip(np.rint(g / st), -128, 127).astype(np.int8))
+
+
+def w8_weight(rng, M, K):
+    codes = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    scales = (np.abs(rng.standard_normal((M, K // 32))) * 0.002).astype(np.float16).view(np.uint16)
+    return codes, scales
+
+
+def test_w8a8_exact_case():
+    # exact-rational: power-of-two scales and small activation codes keep every
+    # FP32 step exact, so GEMV (alternating chains) and GEMM agree with the
+    # int64 product sum_kt d_kt * ws_kt * as_kt
+    rng = np.random.default_rng(33)
+    M, K, T = 32, 512, 3
+    codes = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    e = rng.integers(-6, 0, (M, K // 32))
+    scales = np.exp2(e).astype(np.float16).view(np.uint16)
+    q = rng.integers(-3, 4, (T, K)).astype(np.int8)
+    sm = q.reshape(T, K // 32, 32).sum(axis=2).astype(np.int32)
+    s = np.exp2(rng.integers(-4, 2, (T, K // 32))).astype(np.float32)
+    d = np.einsum("mkj,tkj->tmk", codes.reshape(M, K // 32, 32).astype(np.int64),
+                  q.reshape(T, K // 32, 32).astype(np.int64))
+    want = (d * np.exp2(e)[None] * s[:, None, :]).sum(axis=2).astype(np.float32)
+    for variant, S in ((O.VAR_GEMV, 1), (O.VAR_GEMV, 4), (O.VAR_GEMM, 1)):
+        y = O.project(codes, scales, 32, O.SCALE_S8, q, s, sm, 32, variant, S)
+        assert np.array_equal(y, want), (variant, S)
+
+
+def test_w8a8_all_ones_gives_K_and_tier_checks():
+    M, K, T = 32, 256, 2
+    codes = np.ones((M, K), np.int8)
+    scales = np.full((M, K // 32), 0x3C00, np.uint16)
+    q = np.ones((T, K), np.int8)
+    s = np.ones((T, K // 32), np.float32)
+    sm = np.full((T, K // 32), 32, np.int32)
+    for variant in (O.VAR_GEMV, O.VAR_GEMM):
+        assert np.all(O.project(codes, scales, 32, O.SCALE_S8, q, s, sm, 32, variant, 2) == K)
+    with pytest.raises(ValueError, match="rc=-1"):          # W8 needs block-32 activations
+        O.project(codes, scales, 32, O.SCALE_S8, q, np.ones(T, np.float32), sm, 0, O.VAR_GEMV, 1)
+    with pytest.raises(ValueError, match="rc=-1"):          # and K32 scales
+        O.project(codes, scales[:, ::2].copy(), 64, O.SCALE_S8, q, s, sm, 32, O.VAR_GEMV, 1)
