@@ -236,6 +236,54 @@ def measure_w4a4(cfg, steps, warmup, eager=False):
     return res
 
 
+LM_HEAD_ROWS = 248320        # ~1.27 GB of int8 codes at K = 5120 (kernels_dpas.cpp:1576-1577)
+
+
+def measure_w8a8(steps, warmup, eager=False, rows=LM_HEAD_ROWS, K=5120, T=8):
+    """The W8A8 tier on its reference use: x_gemm_w8a8 over the spec wave's 8
+    rows against an lm_head-sized int8 weight (decode.cpp:2335-2342), seeded
+    synthetic codes (int8 uniform) and FP16 scales |N(0,1)| * 0.002, BF16
+    N(0,1) activations quantized per (token, K32) outside the timed region.
+    HBM-bound: the weight streams once per launch."""
+    import torch
+    from knivesysl_xe_amd import ops
+    from oracle import oracle as O
+    g = torch.Generator(device="cuda").manual_seed(0)
+    codes = torch.randint(-128, 128, (rows, K), dtype=torch.int8, device="cuda", generator=g)
+    scales = (torch.randn(rows, K // 32, device="cuda", generator=g).abs() * 0.002).half().view(torch.int16)
+    w = ops.W4Weight.from_codes_s8(codes, scales)
+    x = torch.randn(T, K, device="cuda", generator=g).bfloat16()
+    act = ops.quantize_act(x, 32)
+    out = torch.empty(T, rows, dtype=torch.float32, device="cuda")
+    copies, rot_bytes = make_copies([w])
+    run = lambda ws: ops.gemm(ws[0], act, torch.float32, forced_splits=1, out=out)
+    secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
+    run(copies[0])
+    torch.cuda.synchronize()
+    c = codes[:512].cpu().numpy()
+    sc = scales[:512].cpu().numpy().view(np.uint16)
+    q, s, sm = O.quantize_act(x.float().cpu().numpy(), 32)
+    ref = O.project(c, sc, 32, O.SCALE_S8, q, s, sm, 32, O.VAR_GEMM, 1)
+    exact = bool(np.array_equal(out[:, :512].cpu().numpy().view(np.uint32), ref.view(np.uint32)))
+    per = secs / steps
+    nbytes = rows * K + rows * (K // 32) * 2 + T * K + T * rows * 4
+    res = {
+        "kernel_us": per * 1e6,
+        "GBps": nbytes / per / 1e9,
+        "TOPS": 2 * T * rows * K / per / 1e12,
+        "bytes": nbytes,
+        "bound": "hbm",
+        "bit_exact_vs_oracle_rows0_512": exact,
+        "rotated_weight_bytes": rot_bytes,
+        "wall_s": wall,
+        "shape": f"T={T} (spec wave), K={K}, N={rows} int8 (lm_head)",
+    }
+    res["roofline_frac"] = res["GBps"] / HBM_PEAK_GBS
+    del copies, w, out, codes
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, budget_s=10.0):
     """The oracle on the host cores over repeated full passes of `cfg`."""
     from oracle import oracle as O
@@ -301,6 +349,7 @@ def main():
                     help="extra BASELINE configs to report ('' for none)")
     ap.add_argument("--w4a4", default="cfg2_m512",
                     help="K64 configs to also run through the W4A4 GEMM ('' for none)")
+    ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
     ap.add_argument("--extra-steps", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
@@ -333,6 +382,11 @@ def main():
         log(f"{name}_w4a4: W4A4 GEMM on the {name} shape (s4 activations, FP16|zp K64 weight)")
         e = extra[f"{name}_w4a4"] = measure_w4a4(cfg, args.extra_steps, 5, args.eager)
         log(f"{name}_w4a4: {e['kernel_us']:.2f} us, {e['TOPS']:.1f} TOPS, frac {e['roofline_frac']:.3f}, "
+            f"exact={e['bit_exact_vs_oracle_rows0_512']}")
+    if not args.no_w8a8:
+        log("lm_head_w8a8: W8A8 GEMM, spec wave T=8, K=5120, N=248320 int8")
+        e = extra["lm_head_w8a8"] = measure_w8a8(20, 3, args.eager)
+        log(f"lm_head_w8a8: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, frac {e['roofline_frac']:.3f}, "
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     if args.copy_mib:
         calibration_copy(args.copy_mib)

@@ -398,6 +398,11 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     if (a.w8) {
         if (unit != 32 || mode != 1) return 1;
         const bool alt2 = a.variant == kVarGemv;
+        if (pf8)
+            return a.T <= 8 ? (alt2 ? rw_launch<8, 32, 1, true, 8, true>(a, grid, block, lds, st)
+                                    : rw_launch<8, 32, 1, false, 8, true>(a, grid, block, lds, st))
+                            : (alt2 ? rw_launch<16, 32, 1, true, 8, true>(a, grid, block, lds, st)
+                                    : rw_launch<16, 32, 1, false, 8, true>(a, grid, block, lds, st));
         if (a.T <= 8)
             return alt2 ? rw_launch<8, 32, 1, true, 4, true>(a, grid, block, lds, st)
                         : rw_launch<8, 32, 1, false, 4, true>(a, grid, block, lds, st);
