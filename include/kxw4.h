@@ -66,7 +66,8 @@ enum { KXW4_F32 = 0, KXW4_BF16 = 1 };
  * l owns bytes [1024h + 16l, +16) of row rg*16 + l%16, holding K32 units
  * j = 2h (bytes 0..7) and 2h+1 (bytes 8..15), byte b of unit j being
  * k = kb*128 + 32j + 8(l/16) + b (the K slots the W4 unpack produces).
- * Requires M % 16 == 0, K % 128 == 0, group in {32, 64, 128} (32 for W8). */
+ * Requires M % 16 == 0, K % 128 == 0, group in {16, 32, 64, 128} (32 for W8;
+ * 16 is the K16 tier: FP16|zp scales, GEMV only). */
 typedef struct kxw4_weight {
     int32_t M, K, group, scale_enc;
     const uint8_t *codes;
@@ -129,7 +130,7 @@ int kxw4_repack_e2m3_s8(const uint8_t *payload, const float *block_scale_inv,
 
 /* Reference DPAS layout (lane-major K32 tiles and FP16|zp scales
  * [M/16][K/group][16], kernels_dpas.cpp:294-342) -> packed layout. Scales are
- * copied bit for bit; group is 32 or 64 (s4_k64). */
+ * copied bit for bit; group is 16 (s4_k16), 32 or 64 (s4_k64). */
 int kxw4_import_ref_weight(const uint8_t *ref_codes, const uint16_t *ref_scales,
                            int M, int K, int group, uint8_t *out_codes,
                            uint16_t *out_scales, void *stream);
@@ -137,8 +138,9 @@ int kxw4_import_ref_weight(const uint8_t *ref_codes, const uint16_t *ref_scales,
 /* x_w4_repack_weight_mode (kernels_dpas.cpp:266-344, 403-424): dense-E2M3
  * fragment payload [M/16][K/32][384 B] and FP32 block scales
  * [ceil(M/128)][scale_cols] -> asymmetric int4 fit per group with the zero
- * point in the FP16 scale nibble. mode 0 = K32 groups, 2 = K64 groups; mode 1
- * (K16) returns KXW4_ETIER. Outputs use KXW4_SCALE_FP16_ZP4. */
+ * point in the FP16 scale nibble. mode 0 = K32 groups, 1 = K16 groups (the
+ * K16 tier, kernels_dpas.cpp:287-296), 2 = K64 groups. Outputs use
+ * KXW4_SCALE_FP16_ZP4. */
 int kxw4_repack_e2m3(const uint8_t *payload, const float *block_scale_inv,
                      int scale_cols, int M, int K, int mode, uint8_t *out_codes,
                      uint16_t *out_scales, void *stream);
@@ -192,14 +194,16 @@ int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4,
  * accumulators per split, ordered split sum, optional FP32 residual[T][M].
  * T in [1, 64]. y is [T][M] of y_dtype. A W8 weight runs x_gemv_w8a8_core's
  * arithmetic (kernels_dpas.cpp:771-844, the same chain with zero point 0) for
- * T in [1, 16]. */
+ * T in [1, 16]. A K16 weight (group 16) runs x_gemv_w4a8_core_k16
+ * (683-760): block-32 activations, two K16 half partials per K32 tile, one
+ * serial accumulator per split, splits on K32 tiles; T in [1, 16]. */
 int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
               const float *residual, int splits, void *stream);
 
 /* x_gemv_w4a8_fanout (kernels_dpas.cpp:945-1102): up to 4 weights with one K
  * and one group/encoding, one launch, serial accumulator, one split count
  * choose_gemv_splits(total row-groups). T in [1, 64]. W8 weights return
- * KXW4_ETIER (the reference has no W8 fan-out). */
+ * KXW4_ETIER (the reference has no W8 fan-out), K16 weights -2 (956-959). */
 int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
                      const kxw4_act_t *a, int y_dtype, void *stream);
 

@@ -56,8 +56,8 @@ typedef struct {
 
 extern "C" void kxw4_compat_set_stream(void *stream);
 
-// kernels_dpas.cpp:403-424. mode 0 = K32 groups, 2 = K64 groups; mode 1
-// (K16) returns KXW4_ETIER. Allocates d_s4/d_s4_scale, frees d_A and
+// kernels_dpas.cpp:403-424. mode 0 = K32 groups, 1 = K16 groups (the K16
+// tier: GEMV only), 2 = K64 groups. Allocates d_s4/d_s4_scale, frees d_A and
 // d_block_scale_inv, synchronizes.
 int x_w4_repack_weight(tq_qmma_weight_t *w);
 int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode);

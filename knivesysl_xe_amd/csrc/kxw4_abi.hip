@@ -12,7 +12,8 @@ namespace {
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
-bool valid_group(int g) { return g == 32 || g == 64 || g == 128; }
+// 16 is the K16 tier (FP16|zp scales, GEMV only)
+bool valid_group(int g) { return g == 16 || g == 32 || g == 64 || g == 128; }
 
 // Shape of one packed weight (x_w4_repack_weight_mode, kernels_dpas.cpp:406).
 bool valid_shape(int M, int K, int group) {
@@ -25,8 +26,10 @@ int check_weight(const kxw4_weight_t *w) {
     if (w->scale_enc != KXW4_SCALE_FP16 && w->scale_enc != KXW4_SCALE_FP16_ZP4 &&
         w->scale_enc != KXW4_SCALE_W8)
         return KXW4_ETIER;
-    // the W8A8 tier keeps one scale per K32 (kernels_dpas.cpp:346-399)
+    // the W8A8 tier keeps one scale per K32 (kernels_dpas.cpp:346-399), the
+    // K16 tier FP16|zp scales (287-296)
     if (w->scale_enc == KXW4_SCALE_W8 && w->group != 32) return KXW4_ESHAPE;
+    if (w->group == 16 && w->scale_enc != KXW4_SCALE_FP16_ZP4) return KXW4_ESHAPE;
     return KXW4_OK;
 }
 
@@ -111,6 +114,8 @@ int gemm_common(const kxw4_weight_t *const *ws, void *const *ys, int count, cons
         if (ws[i]->K != ws[0]->K || ws[i]->group != ws[0]->group ||
             ws[i]->scale_enc != ws[0]->scale_enc)
             return KXW4_ESHAPE;
+        // the K16 tier has no GEMM (x_gemm_w4a8 returns -1, kernels_dpas.cpp:1337)
+        if (ws[i]->group == 16) return KXW4_EARG;
     }
     if (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16) return KXW4_ESHAPE;
     const int rc = check_act(a, ws[0]->K, ws[0]->scale_enc);
@@ -252,10 +257,9 @@ int kxw4_repack_e2m3(const uint8_t *payload, const float *block_scale_inv, int s
         return KXW4_EARG;
     if (M <= 0 || K <= 0 || M % 16 || K % 128) return KXW4_ESHAPE;
     if (mode == 2 && ((K / 32) & 1)) return KXW4_EPREP;
-    if (mode == 1) return KXW4_ETIER;
-    if (mode != 0 && mode != 2) return KXW4_ESHAPE;
+    if (mode != 0 && mode != 1 && mode != 2) return KXW4_ESHAPE;
     if (scale_cols != K / 32 && scale_cols != K / 128) return KXW4_ESHAPE;
-    return launch_repack_e2m3(payload, block_scale_inv, scale_cols, M, K, mode == 2 ? 64 : 32,
+    return launch_repack_e2m3(payload, block_scale_inv, scale_cols, M, K, mode == 2 ? 64 : mode == 1 ? 16 : 32,
                               out_codes, out_scales, as_stream(stream));
 }
 
@@ -303,7 +307,8 @@ int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
     rc = check_act(a, w->K, w->scale_enc);
     if (rc) return rc;
     if (a->T > kDecodeMaxT || (y_dtype != KXW4_F32 && y_dtype != KXW4_BF16)) return KXW4_ESHAPE;
-    if (w->scale_enc == KXW4_SCALE_W8 && a->T > 16) return KXW4_ESHAPE;
+    if ((w->scale_enc == KXW4_SCALE_W8 || w->group == 16) && a->T > 16) return KXW4_ESHAPE;
+    if (w->group == 16 && a->block != 32) return KXW4_EARG;   // K16: block-32 activations
     const int S = splits ? splits : kxw4_gemv_splits(w->M / 16);
     if (!valid_split(S)) return KXW4_ESHAPE;
     const kxw4_weight_t *ws[1] = {w};
@@ -324,6 +329,7 @@ int kxw4_gemv_fanout(const kxw4_weight_t *const *ws, void *const *ys, int count,
             w->scale_enc != ws[0]->scale_enc)
             return KXW4_ESHAPE;
         if (w->scale_enc == KXW4_SCALE_W8) return KXW4_ETIER;   // no W8 fan-out in the reference
+        if (w->group == 16) return KXW4_ESHAPE;                 // nor K16 (kernels_dpas.cpp:956-959)
         groups += w->M / 16;
     }
     if (!a || !a->q || !a->scale || a->K != ws[0]->K) return KXW4_EPREP;

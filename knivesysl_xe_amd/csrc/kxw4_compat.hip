@@ -45,7 +45,7 @@ kxw4_weight_t w4_of(const tq_qmma_weight_t *w) {
     kxw4_weight_t d;
     d.M = w->M;
     d.K = w->K;
-    d.group = w->s4_k64 ? 64 : 32;
+    d.group = w->s4_k64 ? 64 : w->s4_k16 ? 16 : 32;
     d.scale_enc = KXW4_SCALE_FP16_ZP4;
     d.codes = w->d_s4;
     d.scales = w->d_s4_scale;
@@ -88,8 +88,8 @@ int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode) {
     if (!w || !w->d_A || !w->d_block_scale_inv || !w->block_scaled || !w->e2m3) return -1;
     if (w->M % 16 || w->K % 128) return -2;
     if (mode == 2 && (w->Kt & 1)) return -3;
-    if (mode != 0 && mode != 2) return KXW4_ETIER;
-    const int group = mode == 2 ? 64 : 32;
+    if (mode != 0 && mode != 1 && mode != 2) return KXW4_ESHAPE;
+    const int group = mode == 2 ? 64 : mode == 1 ? 16 : 32;
     uint8_t *codes = nullptr;
     uint16_t *scales = nullptr;
     if (hipMalloc(&codes, kxw4_code_bytes(w->M, w->K)) != hipSuccess) return KXW4_EHIP;
@@ -111,7 +111,7 @@ int x_w4_repack_weight_mode(tq_qmma_weight_t *w, int mode) {
     w->d_block_scale_inv = nullptr;
     w->d_s4 = codes;
     w->d_s4_scale = scales;
-    w->s4_k16 = 0;
+    w->s4_k16 = mode == 1 ? 1 : 0;
     w->s4_k64 = mode == 2 ? 1 : 0;
     w->s4_ready = 1;
     return 0;
@@ -176,7 +176,8 @@ void x_rmsnorm_chunk(float *d_out, const float *d_in, const uint16_t *d_w, int H
 }
 
 int x_gemv_w4a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual) {
-    if (!w4_ready(w) || !d_y) return -1;
+    // every W4 tier, K16 included (kernels_dpas.cpp:1647-1653)
+    if (!w || !w->s4_ready || !w->d_s4 || !w->d_s4_scale || !d_y) return -1;
     if (g_act.K != w->K) return -2;
     const kxw4_weight_t d = w4_of(w);
     const kxw4_act_t a = prepared_act();

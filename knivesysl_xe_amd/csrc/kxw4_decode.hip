@@ -332,9 +332,9 @@ int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
     // KXW4_DECODE_KERNEL=persist tries the persistent kernel first (up to 8
     // tokens with one split plan per weight); =kparallel skips the row-wave
     // kernel (used by the tests to cover every kernel at the decode shapes).
-    // W8 weights run on the row-wave kernel only; 1 hands the shape back to
-    // the caller (the GEMM path)
-    if (a.w8) return debug ? 1 : launch_rowwave(a, st);
+    // W8 and K16 weights run on the row-wave kernel only; 1 hands the shape
+    // back to the caller (the GEMM path for W8)
+    if (a.w8 || a.group == 16) return debug ? 1 : launch_rowwave(a, st);
     const char *force = getenv("KXW4_DECODE_KERNEL");
     const bool use_persist = force && strcmp(force, "persist") == 0;
     const bool no_rowwave = force && strcmp(force, "kparallel") == 0;

@@ -1,6 +1,7 @@
 // kxw4_pack.hip — load-time weight kernels: pack natural int4 codes into the
 // gfx950 tile layout, unpack it, import the reference's DPAS layout, and the
-// E2M3 -> asymmetric int4 repack (kernels_dpas.cpp:229-344).
+// E2M3 -> asymmetric int4 repack (kernels_dpas.cpp:229-344; K32, K16 and
+// K64 groups), and the W8A8 tier's int8 pack and repack.
 //
 // Packed tile (16 rows x 128 K, 1024 bytes): lane l owns bytes [16l, 16l+16),
 // row l%16; dword i of the lane holds k = 32i + 8(l/16) + b with b = 0..3 in
@@ -305,6 +306,45 @@ __global__ void repack_e2m3_s8_kernel(const uint8_t *__restrict__ payload, const
         }
 }
 
+// Mode 1, the K16 tier (kernels_dpas.cpp:287-296): one thread per (row, K32
+// tile) fits its two K16 halves (FP16|zp each); half h owns dword kt % 4 of
+// lane groups 2h and 2h + 1.
+__global__ void repack_e2m3_k16_kernel(const uint8_t *__restrict__ payload,
+                                       const float *__restrict__ bs, int scale_cols, int M, int K,
+                                       uint32_t *__restrict__ out_codes,
+                                       uint16_t *__restrict__ out_scales) {
+    const int Kt = K / 32, NT = K / kTileK, G = K / 16;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)M * Kt) return;
+    const int row = (int)(i / Kt), kt = (int)(i % Kt);
+    const int mt = row >> 4, n = row & 15;
+    const int sc = (scale_cols == Kt) ? kt : (kt >> 2);
+    const float b = bs[(size_t)(mt >> 3) * scale_cols + sc];
+    float wf[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) wf[j] = e2m3f(e2m3_code_at(payload, Kt, row, kt * 32 + j)) * b;
+    uint8_t q4[32];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        int z = 0;
+        const uint16_t sh = fit_int4_asym<16>(wf + 16 * h, &z);
+        out_scales[((size_t)mt * G + 2 * kt + h) * 16 + n] = (uint16_t)(sh | (z & 0xF));
+        const float gs = half_bits_to_float(sh);
+#pragma unroll
+        for (int j = 16 * h; j < 16 * h + 16; ++j)
+            q4[j] = (uint8_t)((int)clampf(rintf(wf[j] / gs + (float)z), -8.0f, 7.0f) & 0xF);
+    }
+    uint32_t *tile = out_codes + ((size_t)mt * NT + kt / 4) * 256;
+#pragma unroll
+    for (int gl = 0; gl < 4; ++gl) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb)
+            w |= ((uint32_t)q4[8 * gl + bb] | ((uint32_t)q4[8 * gl + bb + 4] << 4)) << (8 * bb);
+        tile[(n + 16 * gl) * 4 + (kt & 3)] = w;
+    }
+}
+
 static inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 int launch_pack_s8(const int8_t *codes, const uint16_t *scales, int M, int K, uint8_t *out_codes,
@@ -372,7 +412,10 @@ int launch_repack_e2m3(const uint8_t *payload, const float *bs, int scale_cols, 
                        int group, uint8_t *out_codes, uint16_t *out_scales, hipStream_t st) {
     const size_t n = (size_t)M * (K / group);
     uint32_t *oc = reinterpret_cast<uint32_t *>(out_codes);
-    if (group == 32)
+    if (group == 16)
+        hipLaunchKernelGGL(repack_e2m3_k16_kernel, dim3(blocks_for((size_t)M * (K / 32), 128)), dim3(128), 0,
+                           st, payload, bs, scale_cols, M, K, oc, out_scales);
+    else if (group == 32)
         hipLaunchKernelGGL(repack_e2m3_kernel<32>, dim3(blocks_for(n, 128)), dim3(128), 0, st,
                            payload, bs, scale_cols, M, K, oc, out_scales);
     else

@@ -25,6 +25,13 @@
 // used as the K32 MFMA operand without an unpack; the MFMA result is the unit
 // partial itself (no factor 16) and the chain is the reference mode's with
 // zero point 0.
+//
+// K16 (the K16 tier, x_gemv_w4a8_core_k16, kernels_dpas.cpp:683-760): GEMV
+// only, FP16|zp scales per K16 half. A K32 unit's lane groups 0-1 hold half 0
+// and 2-3 half 1, so two MFMAs with the other half's lanes zeroed give the two
+// half partials; each lane's zero point is folded into its weight bytes
+// (w - zp, so no activation sums are needed and the partials carry no factor
+// 16); one serial accumulator per split, which covers whole K32 tiles.
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
@@ -37,12 +44,16 @@ constexpr int kRwWaves = 8;                 // waves per work-group by default
 constexpr int kRwMaxWaves = 16;
 constexpr size_t kRwLdsMax = 160 * 1024;
 
-template <int TT, int UNIT, int MODE, bool ALT2, int PF, bool W8>
+enum { kWfW4 = 0, kWfW8 = 1, kWfK16 = 2 };     // weight format of a row-wave instance
+
+template <int TT, int UNIT, int MODE, bool ALT2, int PF, int WF>
 __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeArgs a) {
     constexpr int UPS = kTileK / UNIT;
-    static_assert(!W8 || (UNIT == 32 && MODE == 1), "W8: K32 units, reference mode");
+    constexpr bool W8 = WF == kWfW8, K16 = WF == kWfK16;
+    static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
+    static_assert(!K16 || ALT2, "K16 is a GEMV");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
-    constexpr float kInv16 = W8 ? 1.0f : 0.0625f;  // undoes the nibble unpack's factor 16
+    constexpr float kInv16 = WF != kWfW4 ? 1.0f : 0.0625f;  // undoes the nibble unpack's factor 16
     static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -58,7 +69,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     const int R = (W.M / 16 + W.wg_count - 1) / W.wg_count;
     const int K = a.K, T = a.T, M = W.M;
     const int NT = K / kTileK, Nu = K / UNIT, G = K / a.group;
-    const int gsh = __builtin_ctz(a.group / UNIT);
+    const int gsh = a.group >= UNIT ? __builtin_ctz(a.group / UNIT) : 0;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, n = lane & 15, g4 = lane >> 4;
@@ -125,7 +136,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
     __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * TB));
-    const bool ref_block = a.block == 32, zp = a.scale_enc == 1;
+    const bool ref_block = a.block == 32, zp = a.scale_enc == 1 && !K16;
     if (MODE != 0) {
         // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
         for (int x = tid; x < Nu * 16; x += nthreads) {
@@ -193,7 +204,27 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                             const long av = (j & 1) ? (long)(((uint64_t)(uint32_t)c.w << 32) | (uint32_t)c.z)
                                                     : (long)(((uint64_t)(uint32_t)c.y << 32) | (uint32_t)c.x);
                             long bv;
-                            if constexpr (W8) {
+                            if constexpr (K16) {
+                                // the unit's two K16 scale words; lane groups
+                                // 0-1 carry half 0, 2-3 half 1
+                                const uint32_t s0 = *(in ? &sbase[(2 * u) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+                                const uint32_t s1 = *(in ? &sbase[(2 * u + 1) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+                                const uint32_t x = (j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w) ^ 0x88888888u;
+                                const uint32_t cz = (uint32_t)(120 - sext4(g4 < 2 ? s0 : s1)) * 0x01010101u;
+                                const uint64_t lo = ((x & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
+                                const uint64_t hi = (((x >> 4) & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
+                                bv = (long)(lo | (hi << 32));
+                                const v4i ph[2] = {mfma_k32(av, g4 < 2 ? bv : 0l, zero), mfma_k32(av, g4 < 2 ? 0l : bv, zero)};
+                                const float4 asv = *reinterpret_cast<const float4 *>(in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4);
+                                const float avr[4] = {asv.x, asv.y, asv.z, asv.w};
+#pragma unroll
+                                for (int h = 0; h < 2; ++h) {
+                                    const float w = half_bits_to_float((uint16_t)((h ? s1 : s0) & 0xFFF0u));
+#pragma unroll
+                                    for (int r = 0; r < 4; ++r) f0[r] = __builtin_fmaf((float)ph[h][r] * w, avr[r], f0[r]);
+                                }
+                                continue;
+                            } else if constexpr (W8) {
                                 const v4u h = ring[p][j >> 1];
                                 bv = (j & 1) ? (long)(((uint64_t)h.w << 32) | h.z)
                                              : (long)(((uint64_t)h.y << 32) | h.x);
@@ -253,7 +284,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
             for (; ib < ntw; ib += PF) ring_pass(ib, std::true_type{});
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float v = ALT2 ? f0[r] + f1[r] : f0[r];
+                const float v = (ALT2 && !K16) ? f0[r] + f1[r] : f0[r];
                 // split 0 stays in the registers of the wave that adds the splits
                 if (S > 1 && s > 0) Part[((rgl * (S - 1) + s - 1) * 4 + r) * 64 + lane] = v;
                 else res[r] = v;
@@ -289,9 +320,9 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     }
 }
 
-template <int TT, int UNIT, int MODE, bool ALT2, int PF, bool W8 = false>
+template <int TT, int UNIT, int MODE, bool ALT2, int PF, int WF = kWfW4>
 static int rw_launch(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-    auto k = rowwave_kernel<TT, UNIT, MODE, ALT2, PF, W8>;
+    auto k = rowwave_kernel<TT, UNIT, MODE, ALT2, PF, WF>;
     static bool attr = false;
     if (!attr) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -399,15 +430,20 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         if (unit != 32 || mode != 1) return 1;
         const bool alt2 = a.variant == kVarGemv;
         if (pf8)
-            return a.T <= 8 ? (alt2 ? rw_launch<8, 32, 1, true, 8, true>(a, grid, block, lds, st)
-                                    : rw_launch<8, 32, 1, false, 8, true>(a, grid, block, lds, st))
-                            : (alt2 ? rw_launch<16, 32, 1, true, 8, true>(a, grid, block, lds, st)
-                                    : rw_launch<16, 32, 1, false, 8, true>(a, grid, block, lds, st));
+            return a.T <= 8 ? (alt2 ? rw_launch<8, 32, 1, true, 8, kWfW8>(a, grid, block, lds, st)
+                                    : rw_launch<8, 32, 1, false, 8, kWfW8>(a, grid, block, lds, st))
+                            : (alt2 ? rw_launch<16, 32, 1, true, 8, kWfW8>(a, grid, block, lds, st)
+                                    : rw_launch<16, 32, 1, false, 8, kWfW8>(a, grid, block, lds, st));
         if (a.T <= 8)
-            return alt2 ? rw_launch<8, 32, 1, true, 4, true>(a, grid, block, lds, st)
-                        : rw_launch<8, 32, 1, false, 4, true>(a, grid, block, lds, st);
-        return alt2 ? rw_launch<16, 32, 1, true, 4, true>(a, grid, block, lds, st)
-                    : rw_launch<16, 32, 1, false, 4, true>(a, grid, block, lds, st);
+            return alt2 ? rw_launch<8, 32, 1, true, 4, kWfW8>(a, grid, block, lds, st)
+                        : rw_launch<8, 32, 1, false, 4, kWfW8>(a, grid, block, lds, st);
+        return alt2 ? rw_launch<16, 32, 1, true, 4, kWfW8>(a, grid, block, lds, st)
+                    : rw_launch<16, 32, 1, false, 4, kWfW8>(a, grid, block, lds, st);
+    }
+    if (a.group == 16) {
+        if (unit != 32 || mode != 1 || a.variant != kVarGemv) return 1;
+        return a.T <= 8 ? rw_launch<8, 32, 1, true, 4, kWfK16>(a, grid, block, lds, st)
+                        : rw_launch<16, 32, 1, true, 4, kWfK16>(a, grid, block, lds, st);
     }
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, block, lds, st);
     return rw_unit<16>(a, unit, mode, pf8, grid, block, lds, st);

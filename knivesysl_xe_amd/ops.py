@@ -122,7 +122,8 @@ class W4Weight:
     @classmethod
     def repack_e2m3(cls, payload: torch.Tensor, block_scale_inv: torch.Tensor, scale_cols: int,
                     M: int, K: int, mode: int) -> "W4Weight":
-        group = 64 if mode == 2 else 32
+        """x_w4_repack_weight_mode: mode 0 = K32, 1 = K16 (the K16 tier), 2 = K64."""
+        group = {0: 32, 1: 16, 2: 64}.get(mode, 32)
         w = cls.empty(M, K, group, SCALE_FP16_ZP4, payload.device)
         check("kxw4_repack_e2m3", lib().kxw4_repack_e2m3(
             _ptr(payload), _ptr(block_scale_inv), scale_cols, M, K, mode, _ptr(w.codes),

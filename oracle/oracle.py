@@ -185,7 +185,7 @@ def repack_e2m3(payload, block_scale_inv, scale_cols: int, M: int, K: int, mode:
                 contract: bool = True):
     payload = _c(payload, np.uint8)
     bs = _c(block_scale_inv, np.float32)
-    group = 64 if mode == 2 else 32
+    group = {0: 32, 1: 16, 2: 64}[mode]
     codes = np.empty((M, K), np.int8)
     scales = np.empty((M, K // group), np.uint16)
     rc = lib().orc_repack_e2m3(_ptr(payload), _ptr(bs), scale_cols, M, K, mode, int(contract),

@@ -285,9 +285,9 @@ int orc_repack_e2m3(const uint8_t *payload, const float *bs, int scale_cols, int
                     int K, int mode, int contract, int8_t *codes, uint16_t *scales) {
     if (!payload || !bs || !codes || !scales) return -1;
     if (M % 16 || K % 128) return -2;
-    if (mode != 0 && mode != 2) return -4;
+    if (mode != 0 && mode != 1 && mode != 2) return -4;
     const int Kt = K / 32;
-    const int group = mode == 2 ? 64 : 32;
+    const int group = mode == 2 ? 64 : mode == 1 ? 16 : 32;   // mode 1: K16 halves (kernels_dpas.cpp:287-296)
     const int G = K / group;
     for (int row = 0; row < M; ++row) {
         const int mt = row >> 4;
@@ -440,6 +440,7 @@ int orc_segment_splits(const int *offsets, int segments, int T, int M, int K, in
 // ---- projection -----------------------------------------------------------
 
 static int unit_of(const orc_weight_t *w, const orc_act_t *a) {
+    if (w->group == 16) return 16;   // the K16 tier: one partial per K16 half
     return a->block == 32 ? 32 : a->block == 64 ? 64 : w->group;
 }
 
@@ -449,7 +450,10 @@ static int act_block_of(const orc_act_t *a) { return a->block == 64 ? 64 : 32; }
 static int check_args(const orc_weight_t *w, const orc_act_t *a) {
     if (!w || !a || !w->codes || !w->scales || !a->q || !a->scale) return -1;
     if (w->M <= 0 || w->M % 16 || w->K <= 0 || w->K % 128 || w->K != a->K) return -2;
-    if (w->group != 32 && w->group != 64 && w->group != 128) return -2;
+    if (w->group != 16 && w->group != 32 && w->group != 64 && w->group != 128) return -2;
+    // the K16 tier (kernels_dpas.cpp:677-760): FP16|zp scales per K16 and
+    // block-32 activations
+    if (w->group == 16 && (w->scale_enc != ORC_SCALE_FP16_ZP4 || a->block != 32)) return -1;
     if (a->block != 0 && a->block != 32 && a->block != 64) return -2;
     // block 64 = s4 activations of the W4A4 GEMM (kernels_dpas.cpp:1503-1504):
     // K64-tier weights with FP16|zp scales only
@@ -479,8 +483,14 @@ static inline int32_t unit_partial(const orc_weight_t *w, const orc_act_t *a, in
         z = sext4(w->scales[(size_t)n * (K / w->group) + g]);
         const int ab = act_block_of(a);
         int32_t s = 0;
-        for (int b = (u * unit) / ab; b < ((u + 1) * unit) / ab; ++b)
-            s += a->sum[(size_t)t * (K / ab) + b];
+        if (unit < ab) {
+            // a K16 half: its own code sum (the reference's per-K16 d_sum,
+            // kernels_dpas.cpp:208-214)
+            for (int j = 0; j < unit; ++j) s += ar[j];
+        } else {
+            for (int b = (u * unit) / ab; b < ((u + 1) * unit) / ab; ++b)
+                s += a->sum[(size_t)t * (K / ab) + b];
+        }
         d -= z * s;
     }
     *zero_point = z;
@@ -513,6 +523,9 @@ int orc_partials(const orc_weight_t *w, const orc_act_t *a, int32_t *P) {
 // (1030-1074, 1313-1321, 1450-1468). Splits cover units [Nu*s/S, Nu*(s+1)/S);
 // S == 1 stores the chain directly, otherwise 0 + partial_0 + ... in split
 // order (663-672, 1092-1101, 1477-1486).
+// K16 tier (x_gemv_w4a8_core_k16, 683-760): GEMV only, one serial
+// accumulator, splits over K32 tiles [Kt*s/S, Kt*(s+1)/S) each covering both
+// K16 halves, as per K32.
 int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
                 const int *split_per_token, int contract, const float *residual,
                 int out_bf16, void *y, int row_begin, int row_end) {
@@ -524,6 +537,9 @@ int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
     if (variant == ORC_VAR_FANOUT && residual) return -2;
     // W4A4: the GEMM variant, one chain per output (kernels_dpas.cpp:1540-1568)
     if (a->block == 64 && variant != ORC_VAR_GEMM) return -2;
+    // K16: GEMV only (x_gemm_w4a8 rejects it, kernels_dpas.cpp:1337)
+    if (w->group == 16 && variant != ORC_VAR_GEMV) return -1;
+    const bool k16 = w->group == 16;
     const int M = w->M, K = w->K, T = a->T;
     if (row_begin < 0 || row_end > M || row_begin > row_end) return -2;
     const int unit = unit_of(w, a), Nu = K / unit, G = K / w->group;
@@ -544,19 +560,21 @@ int orc_project(const orc_weight_t *w, const orc_act_t *a, int variant,
                 const int S = split_per_token[t];
                 float sum = 0.0f;
                 for (int s = 0; s < S; ++s) {
-                    const int u0 = (int)((long long)Nu * s / S);
-                    const int u1 = (int)((long long)Nu * (s + 1) / S);
+                    const int step = k16 ? 2 : 1;   // K16: splits on K32 tiles
+                    const int u0 = step * (int)((long long)(Nu / step) * s / S);
+                    const int u1 = step * (int)((long long)(Nu / step) * (s + 1) / S);
                     float acc0 = 0.0f, acc1 = 0.0f;
                     for (int u = u0; u < u1; ++u) {
                         const uint16_t raw = w->scales[(size_t)n * G + (u * unit) / w->group];
                         const float ws = orc_f16_to_f32(
                             w->scale_enc == ORC_SCALE_FP16_ZP4 ? (uint16_t)(raw & 0xFFF0u) : raw);
                         const float p = (float)P[u];
-                        float &acc = (variant == ORC_VAR_GEMV && ((u - u0) & 1)) ? acc1 : acc0;
+                        float &acc = (variant == ORC_VAR_GEMV && !k16 && ((u - u0) & 1)) ? acc1 : acc0;
                         if (per_token) {
                             acc = contract ? std::fma(p, ws, acc) : acc + p * ws;
                         } else {
-                            const float as = a->scale[(size_t)t * (K / act_block_of(a)) + u];
+                            const float as = a->scale[(size_t)t * (K / act_block_of(a)) +
+                                                      (u * unit) / act_block_of(a)];
                             if (variant == ORC_VAR_GEMM) {
                                 const float wa = ws * as;
                                 acc = contract ? std::fma(p, wa, acc) : acc + p * wa;

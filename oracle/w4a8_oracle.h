@@ -20,6 +20,10 @@
  *                    (ORC_SCALE_S8) and block-32 activations: the reference
  *                    mode arithmetic with zero point 0 (kernels_dpas.cpp:
  *                    771-844 GEMV, 1578-1629 GEMM).
+ *   K16 tier       : FP16|zp scales per K16 half, block-32 activations, the
+ *                    GEMV only: per K32 tile two half partials, one serial
+ *                    accumulator, splits on K32 tiles (kernels_dpas.cpp:
+ *                    683-760).
  *   W4A4 mode      : s4 activations (block 64: codes in [-7, 7], one FP32
  *                    scale and one code sum per (token, K64)), K64 weights
  *                    with FP16|zp scales, the GEMM variant (x_gemm_w4a4,
@@ -107,7 +111,8 @@ void orc_rmsnorm(const float *in, const uint16_t *w_bf16, int H, float eps,
 uint16_t orc_fit_int4_asym(const float *wf, int n, int reserve_nibble,
                            int contract, int *out_z);
 /* E2M3 fragment payload + block scales -> natural int4 codes [M][K] and
- * packed FP16|zp scales [M][K/group]; mode 0 = K32 groups, 2 = K64. */
+ * packed FP16|zp scales [M][K/group]; mode 0 = K32 groups, 1 = K16 (the K16
+ * tier), 2 = K64. */
 int orc_repack_e2m3(const uint8_t *payload, const float *block_scale_inv,
                     int scale_cols, int M, int K, int mode, int contract,
                     int8_t *codes, uint16_t *scales);

@@ -75,7 +75,7 @@ static Source make_source(std::mt19937 &rng, int M, int K, int mode) {
     s.bs.resize((size_t)((M + 127) / 128) * s.scale_cols);
     std::uniform_real_distribution<float> u(0.001f, 0.05f);
     for (auto &v : s.bs) v = u(rng);
-    const int group = mode == 2 ? 64 : 32;
+    const int group = mode == 2 ? 64 : mode == 1 ? 16 : 32;
     s.codes.resize((size_t)M * K);
     s.scales.resize((size_t)M * (K / group));
     // contract = 1: the device fit contracts its multiply-adds as icpx would
@@ -107,7 +107,7 @@ static orc_weight_t oracle_weight(const Source &s) {
     orc_weight_t o;
     o.M = s.M;
     o.K = s.K;
-    o.group = s.mode == 2 ? 64 : 32;
+    o.group = s.mode == 2 ? 64 : s.mode == 1 ? 16 : 32;
     o.scale_enc = ORC_SCALE_FP16_ZP4;
     o.codes = s.codes.data();
     o.scales = s.scales.data();
@@ -292,6 +292,30 @@ int main() {
         HIPCHECK(hipFree(das4));
         HIPCHECK(hipFree(dsum4));
         HIPCHECK(hipFree(dy4));
+    }
+
+    // ---- K16 tier: x_w4_repack_weight_mode(w, 1) and the K16 GEMV ---------
+    {
+        Source s16 = make_source(rng, 256, 2048, 1);
+        tq_qmma_weight_t w16 = make_weight(s16);
+        check(x_w4_repack_weight_mode(&w16, 1) == 0 && w16.s4_k16 && !w16.s4_k64, "x_w4_repack_weight_mode K16");
+        orc_weight_t o16{256, 2048, 16, ORC_SCALE_FP16_ZP4, s16.codes.data(), s16.scales.data()};
+        std::vector<int8_t> q(2048);
+        std::vector<float> sc(64);
+        std::vector<int32_t> sm(64);
+        orc_quantize_act(x.data(), 1, 2048, 32, q.data(), sc.data(), sm.data());
+        orc_act_t a{1, 2048, 32, q.data(), sc.data(), sm.data()};
+        const std::vector<int> sp(1, orc_gemv_splits(256 / 16));
+        std::vector<float> y(256, 0.0f), yr(256, 0.0f);
+        orc_project(&o16, &a, ORC_VAR_GEMV, sp.data(), 1, nullptr, 0, y.data(), 0, 256);
+        orc_project(&o16, &a, ORC_VAR_GEMV, sp.data(), 1, res.data(), 0, yr.data(), 0, 256);
+        check(x_gemv_w4a8(&w16, dx, dy) == 0 && same_bits(host_copy(dy, 256), y), "x_gemv_w4a8 K16 == oracle");
+        check(x_gemv_w4a8_add(&w16, dx, dres, dy) == 0 && same_bits(host_copy(dy, 256), yr),
+              "x_gemv_w4a8_add K16 == oracle");
+        const tq_qmma_weight_t *k16s[2] = {&w16, &w16};
+        float *k16y[2] = {dy, dy2};
+        check(x_gemv_w4a8_fanout(k16s, k16y, 2) == -2, "K16 fan-out = -2");
+        check(x_gemm_w4a8(&w16, daq, das, dasum, dyt, T) == -1, "K16 GEMM = -1");
     }
 
     // ---- W8A8 tier: x_w8_repack_weight, GEMV (+add, tier routing), GEMM ---

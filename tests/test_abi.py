@@ -122,10 +122,17 @@ def test_weight_and_quantizer_checks():
     assert L.kxw4_pack_weight(p, p, 24, 128, 32, p, p, None) == _lib.ESHAPE
     assert L.kxw4_import_ref_weight(p, p, 16, 128, 128, p, p, None) == _lib.ESHAPE
     # x_w4_repack_weight_mode: -2 shape (its -3, an odd K32 tile count for
-    # K64, cannot follow a passed K % 128 check); K16 is not built here
+    # K64, cannot follow a passed K % 128 check); modes 0 (K32), 1 (K16) and
+    # 2 (K64) exist
     assert L.kxw4_repack_e2m3(p, p, 4, 16, 100, 0, p, p, None) == _lib.ESHAPE
     assert L.kxw4_repack_e2m3(p, p, 3, 16, 128, 0, p, p, None) == _lib.ESHAPE
-    assert L.kxw4_repack_e2m3(p, p, 4, 16, 128, 1, p, p, None) == _lib.ETIER
+    assert L.kxw4_repack_e2m3(p, p, 4, 16, 128, 3, p, p, None) == _lib.ESHAPE
+    # W8 weights keep K32 scales; K16 weights FP16|zp scales (checked before
+    # any launch)
+    w8 = _lib.Weight(16, 128, 64, _lib.SCALE_W8, 1, 1)
+    w16 = _lib.Weight(16, 128, 16, _lib.SCALE_FP16, 1, 1)
+    assert L.kxw4_unpack_weight(C.byref(w8), p, p, None) == _lib.ESHAPE
+    assert L.kxw4_unpack_weight(C.byref(w16), p, p, None) == _lib.ESHAPE
     assert L.kxw4_quantize_act(None, 0, 1, 128, 0, p, p, p, None) == _lib.EARG
     assert L.kxw4_quantize_act(p, 0, 1, 96, 0, p, p, p, None) == _lib.ESHAPE
     assert L.kxw4_quantize_act(p, 0, 1, 128, 16, p, p, p, None) == _lib.ESHAPE

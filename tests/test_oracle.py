@@ -203,13 +203,13 @@ def decode_payload(payload, bs, scale_cols, M, K):
     return wf
 
 
-@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 def test_repack_e2m3_quantizes_against_stored_scale(mode):
     rng = np.random.default_rng(7 + mode)
     M, K = 32, 256
     payload, bs, scale_cols = random_payload(rng, M, K)
     codes, scales = O.repack_e2m3(payload, bs, scale_cols, M, K, mode)
-    group = 64 if mode == 2 else 32
+    group = {0: 32, 1: 16, 2: 64}[mode]
     wf = decode_payload(payload, bs, scale_cols, M, K)
     ws = O.f16_to_f32(scales & 0xFFF0)
     z = (scales & 0xF).astype(np.int32)
@@ -574,3 +574,73 @@ def test_w8a8_all_ones_gives_K_and_tier_checks():
         O.project(codes, scales, 32, O.SCALE_S8, q, np.ones(T, np.float32), sm, 0, O.VAR_GEMV, 1)
     with pytest.raises(ValueError, match="rc=-1"):          # and K32 scales
         O.project(codes, scales[:, ::2].copy(), 64, O.SCALE_S8, q, s, sm, 32, O.VAR_GEMV, 1)
+
+
+# ---- K16 tier: GEMV over K16 halves -----------------------------------------
+
+def k16_case(terms, as_tiles, K=384):
+    """One weight row whose K16 unit u contributes exactly terms[u] (code w at
+    the unit's first element, activation code 1 there and 0 elsewhere, zero
+    point 0): terms[u] = w * ws_u * as_{u/2}. Returns oracle inputs for T = 1."""
+    Nu = K // 16
+    codes = np.zeros((16, K), np.int8)
+    ws = np.ones((16, Nu), np.float32)
+    q = np.zeros((1, K), np.int8)
+    for u, v in enumerate(terms):
+        if v == 0:
+            continue
+        w = 4 if v / as_tiles[u // 2] >= 4 else 1
+        codes[0, 16 * u] = w
+        ws[0, u] = v / as_tiles[u // 2] / w
+        q[0, 16 * u] = 1
+    scales = (ws.astype(np.float16).view(np.uint16) & 0xFFF0).astype(np.uint16)
+    assert np.all(O.f16_to_f32(scales[0]) == ws[0])
+    s = np.repeat(np.asarray(as_tiles, np.float32)[None, :K // 32], 1, axis=0)
+    sm = q.reshape(1, K // 32, 32).sum(axis=2).astype(np.int32)
+    return codes, scales, q, s, sm
+
+
+def test_k16_splits_fall_on_k32_tiles():
+    # x_gemv_w4a8_core_k16 (kernels_dpas.cpp:712-713) splits K32 tiles: K = 384
+    # (12 tiles) in 8 splits gives tile boundaries 0,1,3,4,...; split 0 holds
+    # units 0-1 (2^24) and split 1 units 2-5 (1 + 1), so the ordered sum is
+    # 2^24 + 2 exactly. Boundaries taken on K16 units (0,3,6,...) would put the
+    # first 1 in split 0, where 2^24 + 1 rounds back to 2^24.
+    terms = [2.0 ** 24, 0, 1.0, 1.0] + [0] * 20
+    codes, scales, q, s, sm = k16_case(terms, [2.0 ** 11, 1.0] + [1.0] * 10)
+    y = O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, 8)
+    assert y[0, 0] == np.float32(2.0 ** 24 + 2)
+
+
+def test_k16_single_serial_accumulator():
+    # one accumulator per split (kernels_dpas.cpp:704, 733-739): units 1, 2^24,
+    # 1 give (1 + 2^24) + 1 = 2^24; the W4A8 GEMV's alternating pair would
+    # give (1 + 1) + 2^24 = 2^24 + 2
+    terms = [1.0, 2.0 ** 24, 1.0] + [0] * 21
+    codes, scales, q, s, sm = k16_case(terms, [2.0 ** 12, 1.0] + [1.0] * 10)
+    y = O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, 1)
+    assert y[0, 0] == np.float32(2.0 ** 24)
+
+
+def test_k16_zero_points_per_half_and_tier_checks():
+    # exact-rational: each K16 half subtracts its own zero point times its own
+    # code sum, then scales by ws_half * as_tile
+    rng = np.random.default_rng(51)
+    M, K, T = 32, 256, 2
+    codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    zp = rng.integers(-8, 8, (M, K // 16))
+    e = rng.integers(-4, 1, (M, K // 16))
+    scales = ((np.exp2(e).astype(np.float16).view(np.uint16) & 0xFFF0) | (zp & 0xF)).astype(np.uint16)
+    q = rng.integers(-3, 4, (T, K)).astype(np.int8)
+    s = np.exp2(rng.integers(-3, 2, (T, K // 32))).astype(np.float32)
+    sm = q.reshape(T, K // 32, 32).sum(axis=2).astype(np.int32)
+    w = codes.reshape(M, K // 16, 16).astype(np.int64) - zp[..., None]
+    d = np.einsum("muk,tuk->tmu", w, q.reshape(T, K // 16, 16).astype(np.int64))
+    want = (d * np.exp2(e)[None] * np.repeat(s, 2, axis=1)[:, None, :]).sum(axis=2).astype(np.float32)
+    for S in (1, 2, 4):
+        y = O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, S)
+        assert np.array_equal(y, want), S
+    with pytest.raises(ValueError, match="rc=-1"):        # GEMV only
+        O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMM, 1)
+    with pytest.raises(ValueError, match="rc=-1"):        # block-32 activations only
+        O.project(codes, scales, 16, 1, q, np.ones(T, np.float32), sm, 0, O.VAR_GEMV, 1)
