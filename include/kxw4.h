@@ -235,6 +235,40 @@ int kxw4_gemm_w4a4(const kxw4_weight_t *w, const uint8_t *q4, const float *scale
                    const int32_t *sum, int T, void *y, int y_dtype,
                    const float *residual, void *stream);
 
+/* ---- TQF1 ingest (host side) ---------------------------------------------
+ * The reference's model container (tqf_loader.cpp:393-626): kxw4_tqf_open
+ * validates the header as the reference does (BF16 non-quant tensors, dense
+ * block-scaled E2M3 QMMA payloads, header size, layer types) and walks the
+ * whole tensor sequence, reading no payload; the file must end exactly where
+ * the sequence does. Each QMMA record (186-255) can then be repacked straight
+ * into caller-owned device buffers: mode 0 / 1 / 2 as kxw4_repack_e2m3 (W4,
+ * K32 / K16 / K64 groups), mode 8 as kxw4_repack_e2m3_s8 (W8A8). Errors: -1
+ * unreadable file, bad magic or index, -2 bad header or shapes, -5 a payload
+ * encoding this library does not ingest, -6 HIP. No counterpart in the
+ * reference's projection interface: it replaces the read_qmma +
+ * x_w4_repack_weight_mode pair of qwn_load. */
+typedef struct kxw4_tqf kxw4_tqf_t;
+enum { KXW4_TQF_BF16 = 0, KXW4_TQF_F32 = 1, KXW4_TQF_QMMA = 2 };
+typedef struct kxw4_tqf_tensor {
+    char name[64];            /* "lm_head", "layer3.mlp_down", "mtp.fc", ... */
+    int32_t kind;             /* KXW4_TQF_* */
+    int32_t M, K;             /* QMMA: rows, cols; vectors: element count, 1 */
+    int32_t scale_rows, scale_cols;   /* QMMA block scales */
+    uint64_t offset, bytes;   /* the record's byte range in the file */
+} kxw4_tqf_tensor_t;
+int kxw4_tqf_open(const char *path, kxw4_tqf_t **out);
+void kxw4_tqf_close(kxw4_tqf_t *t);
+int kxw4_tqf_count(const kxw4_tqf_t *t);
+/* u[16], fl[3] and tail[8] of the header (any may be NULL) */
+int kxw4_tqf_header(const kxw4_tqf_t *t, uint32_t *u16, float *f3, uint32_t *tail8);
+int kxw4_tqf_tensor(const kxw4_tqf_t *t, int index, kxw4_tqf_tensor_t *out);
+/* index of the tensor named `name`, or -1 */
+int kxw4_tqf_find(const kxw4_tqf_t *t, const char *name);
+/* out_codes: kxw4_code_bytes(M, K) (M*K for mode 8); out_scales:
+ * kxw4_scale_count(M, K, group) entries. Synchronizes `stream`. */
+int kxw4_tqf_load_qmma(const kxw4_tqf_t *t, int index, int mode,
+                       uint8_t *out_codes, uint16_t *out_scales, void *stream);
+
 /* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
  * else group), from the same unpack and MFMA code as the projections. */
 int kxw4_partials(const kxw4_weight_t *w, const kxw4_act_t *a, int32_t *P,

@@ -22,6 +22,12 @@ class Weight(C.Structure):
                 ("scale_enc", C.c_int32), ("codes", C.c_void_p), ("scales", C.c_void_p)]
 
 
+class TqfTensor(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("kind", C.c_int32), ("M", C.c_int32), ("K", C.c_int32),
+                ("scale_rows", C.c_int32), ("scale_cols", C.c_int32), ("offset", C.c_uint64),
+                ("bytes", C.c_uint64)]
+
+
 class Act(C.Structure):
     _fields_ = [("T", C.c_int32), ("K", C.c_int32), ("block", C.c_int32),
                 ("q", C.c_void_p), ("scale", C.c_void_p), ("sum", C.c_void_p)]
@@ -54,6 +60,13 @@ SIGNATURES = {
     "kxw4_gemm": (I, [WP, AP, P, I, P, C.POINTER(I), I, I, P]),
     "kxw4_gemm_fanout": (I, [C.POINTER(WP), C.POINTER(P), I, AP, I, C.POINTER(I), I, I, P]),
     "kxw4_gemm_w4a4": (I, [WP, P, P, P, I, P, I, P, P]),
+    "kxw4_tqf_open": (I, [C.c_char_p, C.POINTER(P)]),
+    "kxw4_tqf_close": (None, [P]),
+    "kxw4_tqf_count": (I, [P]),
+    "kxw4_tqf_header": (I, [P, P, P, P]),
+    "kxw4_tqf_tensor": (I, [P, I, C.POINTER(TqfTensor)]),
+    "kxw4_tqf_find": (I, [P, C.c_char_p]),
+    "kxw4_tqf_load_qmma": (I, [P, I, I, P, P, P]),
     "kxw4_partials": (I, [WP, AP, P, P]),
 }
 

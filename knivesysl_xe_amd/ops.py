@@ -17,6 +17,7 @@ of the reference's library-global scratch:
     x_gemv_w4a8_fanout                gemv_fanout
     x_gemm_w4a8                       gemm
     (one launch for gate+up)          gemm_fanout
+    qwn_load's read_qmma + repack     TqfFile.load_w4 / load_w8 (TQF1 ingest)
     x_quantize_act_chunk_s4           quantize_act_s4
     x_gemm_w4a4                       gemm_w4a4
 
@@ -339,6 +340,67 @@ def gemm_w4a4(w: W4Weight, a: QuantActS4, dtype=torch.float32, residual=None,
         C.byref(wc), _ptr(a.q4), _ptr(a.scale), _ptr(a.sum), a.T, _ptr(y), _dtype_code(dtype),
         _ptr(residual), _stream()))
     return y
+
+
+class TqfFile:
+    """A TQF1 model container opened for ingest (tqf_loader.cpp:393-626): the
+    tensor table is read at open, payloads only by load_w4 / load_w8."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        check("kxw4_tqf_open", lib().kxw4_tqf_open(str(path).encode(), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().kxw4_tqf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def header(self):
+        u = (C.c_uint32 * 16)()
+        f = (C.c_float * 3)()
+        t = (C.c_uint32 * 8)()
+        check("kxw4_tqf_header", lib().kxw4_tqf_header(self._h, u, f, t))
+        return list(u), list(f), list(t)
+
+    def tensors(self):
+        out = []
+        for i in range(lib().kxw4_tqf_count(self._h)):
+            d = _lib.TqfTensor()
+            check("kxw4_tqf_tensor", lib().kxw4_tqf_tensor(self._h, i, C.byref(d)))
+            out.append({"name": d.name.decode(), "kind": d.kind, "M": d.M, "K": d.K,
+                        "scale_rows": d.scale_rows, "scale_cols": d.scale_cols,
+                        "offset": d.offset, "bytes": d.bytes})
+        return out
+
+    def find(self, name: str) -> int:
+        i = lib().kxw4_tqf_find(self._h, name.encode())
+        if i < 0:
+            raise KeyError(name)
+        return i
+
+    def _load(self, name: str, mode: int, group: int, scale_enc: int) -> W4Weight:
+        i = self.find(name)
+        d = _lib.TqfTensor()
+        check("kxw4_tqf_tensor", lib().kxw4_tqf_tensor(self._h, i, C.byref(d)))
+        w = W4Weight.empty(d.M, d.K, group, scale_enc)
+        check("kxw4_tqf_load_qmma", lib().kxw4_tqf_load_qmma(
+            self._h, i, mode, _ptr(w.codes), _ptr(w.scales), _stream()))
+        return w
+
+    def load_w4(self, name: str, mode: int = 0) -> W4Weight:
+        """x_w4_repack_weight_mode of one QMMA tensor: 0 = K32, 1 = K16, 2 = K64."""
+        return self._load(name, mode, {0: 32, 1: 16, 2: 64}[mode], SCALE_FP16_ZP4)
+
+    def load_w8(self, name: str) -> W4Weight:
+        """x_w8_repack_weight of one QMMA tensor (the W8A8 tier)."""
+        return self._load(name, 8, 32, SCALE_W8)
 
 
 def partials(w: W4Weight, a: QuantAct) -> torch.Tensor:
