@@ -57,9 +57,22 @@ struct G3Shape {
     static constexpr int B_BYTES = BNG * kTileBytes;
     static constexpr int S_BYTES = BNG * UPS * 32;       // [row-group][unit][16] FP16
     static constexpr int STAGE = (A_BYTES + B_BYTES + S_BYTES + 1023) / 1024 * 1024;
-    static constexpr int A_LOADS = A_BYTES / 1024 / NW;  // 1 KB wave loads per wave and stage
-    static constexpr int B_LOADS = BNG / NW;
-    static constexpr int S_LANES = BNG * UPS * 2 / NW;   // 16-byte scale granules per wave
+    // Loads per wave and stage. Every wave issues the same number (one vmcnt
+    // retires a stage); when the waves do not divide the 1 KB chunks, the
+    // chunk index wraps and a few chunks are loaded twice (same bytes to the
+    // same LDS address).
+    static constexpr int A_CHUNKS = A_BYTES / 1024;
+    static constexpr int A_LOADS = (A_CHUNKS + NW - 1) / NW;
+    static constexpr int B_LOADS = (BNG + NW - 1) / NW;
+    static constexpr int S_TOTAL = BNG * UPS * 2;        // 16-byte scale granules per stage
+    // granules per wave: the smallest divisor of S_TOTAL that covers it with
+    // NW waves, so a wave's wrapped range never straddles the wrap point
+    static constexpr int s_lanes() {
+        int d = (S_TOTAL + NW - 1) / NW;
+        while (S_TOTAL % d) ++d;
+        return d;
+    }
+    static constexpr int S_LANES = s_lanes();
     static constexpr int LOADS = A_LOADS + B_LOADS + 1;
     // output staging: a wave's slab of SB token blocks x 32*TB rows of FP32,
     // token stride EPS floats (EPS = 8 mod 16, so the two K groups of one
@@ -79,9 +92,8 @@ struct G3Shape {
     }
     template <int NST>
     static constexpr int lds_bytes() { return body_bytes<NST>() + BM * 4; }
-    static_assert(A_BYTES % (1024 * NW) == 0, "activation tile splits evenly over the waves");
-    static_assert(BNG % NW == 0, "weight tiles split evenly over the waves");
-    static_assert((BNG * UPS * 2) % NW == 0 && S_LANES <= 64, "scale granules split evenly");
+    static_assert(A_BYTES % 1024 == 0, "activation tile in whole 1 KB chunks");
+    static_assert(S_LANES <= 64, "one scale load per wave and stage");
 };
 
 // OCC: waves per SIMD the register budget is sized for
@@ -125,7 +137,7 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     uint32_t aoffs[S::A_LOADS];
 #pragma unroll
     for (int i = 0; i < S::A_LOADS; ++i) {
-        const int p = (wave + NW * i) * 64 + lane;            // granule this lane fills
+        const int p = ((wave + NW * i) % S::A_CHUNKS) * 64 + lane;            // granule this lane fills
         const int t = 2 * (p >> 4) + ((p >> 3) & 1);
         const int c16 = (p & 7) ^ ((t >> 1) & 7);
         const int tg = min(t0 + t, T - 1);                    // rows past T: never stored
@@ -134,13 +146,13 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     uint32_t boffs[S::B_LOADS];
 #pragma unroll
     for (int i = 0; i < S::B_LOADS; ++i) {
-        const int rg = min(rg0 + wave + NW * i, RG - 1);      // row-groups past M: never stored
+        const int rg = min(rg0 + (wave + NW * i) % BNG, RG - 1);      // row-groups past M: never stored
         boffs[i] = (uint32_t)rg * NT * kTileBytes + lane * 16;
     }
     // scale granule gi = (j * UPS + u) * 2 + half of this wave's slice
     uint32_t soff;
     {
-        const int gi = wave * S::S_LANES + min(lane, S::S_LANES - 1);
+        const int gi = (wave * S::S_LANES + min(lane, S::S_LANES - 1)) % S::S_TOTAL;
         const int j = gi / (2 * UPS), u = (gi >> 1) % UPS, half = gi & 1;
         const int rg = min(rg0 + j, RG - 1);
         soff = ((uint32_t)rg * G + u) * 16 + half * 8;
@@ -154,16 +166,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
 #pragma unroll
         for (int i = 0; i < S::A_LOADS; ++i)
             __builtin_amdgcn_global_load_lds((const void *)(qk + aoffs[i]),
-                                             KXW4_G3_LDS(base + (wave + NW * i) * 1024), 16, 0, 0);
+                                             KXW4_G3_LDS(base + ((wave + NW * i) % S::A_CHUNKS) * 1024), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < S::B_LOADS; ++i)
             __builtin_amdgcn_global_load_lds((const void *)(wk + boffs[i]),
-                                             KXW4_G3_LDS(base + A_BYTES + (wave + NW * i) * 1024), 16, 0, 0);
+                                             KXW4_G3_LDS(base + A_BYTES + ((wave + NW * i) % BNG) * 1024), 16, 0, 0);
         // lanes past the wave's granules are masked off; the load still
         // counts once in vmcnt
         if (lane < S::S_LANES)
             __builtin_amdgcn_global_load_lds((const void *)(W.scales + (size_t)kb * UPS * 16 + soff),
-                                             KXW4_G3_LDS(base + A_BYTES + B_BYTES + wave * S::S_LANES * 16),
+                                             KXW4_G3_LDS(base + A_BYTES + B_BYTES + (wave * S::S_LANES) % S::S_TOTAL * 16),
                                              16, 0, 0);
         // with the first stage, the tile's token scales (64 per wave); the
         // later stages' loads are all younger, so the first wait retires it
@@ -404,21 +416,48 @@ int launch_gemm3(GemmArgs &a, hipStream_t st) {
         for (int s = 0; s < a.seg_count; ++s)
             if (a.w[i].seg_split[s] != 1) return 1;
     }
-    // Tile: 256 x 256 (8 waves, one work-group per CU) where there are at
-    // least four such tiles per CU; below that the grid would leave CUs idle
-    // or unbalanced, and 128 x 64 tiles (4 waves, three work-groups per CU)
-    // fill the chip. KXW4_GEMM3_TILE=0..4 picks one configuration (tests).
+    // Tile choice. Per SIMD the kernel is bound by the FP32 chain of its
+    // blocks, so each candidate is scored by the rounds of work-groups it
+    // needs over the CUs times the 32x32 blocks per K step its busiest SIMD
+    // carries per round (waves on that SIMD x blocks per wave); the small
+    // tile pays ~10% for its larger L2 traffic per MAC (measured):
+    //   256 x 256, 8 waves (2 per SIMD, 8 blocks each), one work-group per CU;
+    //   256 x 160 (G128) / 64 x 160 (G64), 10 waves (3 on the busiest SIMD),
+    //     one work-group per CU: fits the grid when the 256-row tile leaves
+    //     CUs idle;
+    //   128 x 64, 4 waves of 2 blocks, three work-groups per CU.
+    // KXW4_GEMM3_TILE=0..9 picks one configuration (tests, tuning).
     const char *cfg = getenv("KXW4_GEMM3_TILE");
     int sel = cfg ? atoi(cfg) : -1;
     if (sel < 0) {
-        long long big = 0;
-        const int rows = a.group == 128 ? 256 : 128;
-        for (int i = 0; i < a.count; ++i) big += (a.w[i].M + rows - 1) / rows;
-        big *= (a.T + 255) / 256;
-        sel = big >= 4ll * device_cus() ? 0 : (a.group == 128 ? 3 : 4);
+        const bool g128 = a.group == 128;
+        struct Cand { int sel, bm, bng, wgs, simd_blocks; double penalty; };
+        const Cand cands[3] = {
+            {0, 256, g128 ? 16 : 8, 1, g128 ? 16 : 8, 1.0},
+            {g128 ? 9 : 8, g128 ? 256 : 64, 10, 1, g128 ? 12 : 3, 1.0},
+            {g128 ? 3 : 4, 128, 4, 3, 6, 1.1},
+        };
+        const long long cus = device_cus();
+        double best = 0.0;
+        for (const Cand &c : cands) {
+            long long nt = 0;
+            for (int i = 0; i < a.count; ++i) nt += (a.w[i].M / 16 + c.bng - 1) / c.bng;
+            const long long tiles = nt * ((a.T + c.bm - 1) / c.bm);
+            const long long rounds = (tiles + cus * c.wgs - 1) / (cus * c.wgs);
+            const double cost = (double)rounds * c.simd_blocks * c.penalty;
+            if (sel < 0 || cost < best) {
+                best = cost;
+                sel = c.sel;
+            }
+        }
     }
     if (a.group == 128) {
         switch (sel) {
+        case 8: return launch_g3<4, 1, 2, 5, 128, 3, 3>(a, st);   // 256 x 160, 10 waves
+        case 9: return launch_g3<4, 1, 2, 5, 128, 2, 3>(a, st);   // 256 x 160, 10 waves, 2 stages
+        case 5: return launch_g3<2, 2, 2, 2, 128, 3, 2>(a, st);   // 128 x 128, 4 waves
+        case 6: return launch_g3<2, 2, 1, 4, 128, 3, 2>(a, st);   // 64 x 256, 4 waves
+        case 7: return launch_g3<1, 2, 2, 2, 128, 3, 3>(a, st);   // 64 x 128, 4 waves, three per CU
         case 1: return launch_g3<4, 2, 1, 4, 128, 2>(a, st);      // 128 x 256, 4 waves, two per CU
         case 2: return launch_g3<4, 2, 2, 4, 128, 2>(a, st);      // 256 x 256, 8 waves, 2 stages
         case 3: return launch_g3<2, 1, 2, 2, 128, 2, 3>(a, st);   // 128 x 64, 4 waves, three per CU
@@ -427,6 +466,11 @@ int launch_gemm3(GemmArgs &a, hipStream_t st) {
     }
     // group 64: two chain updates per block and step
     switch (sel) {
+    case 8: return launch_g3<1, 1, 2, 5, 64, 3, 3>(a, st);        // 64 x 160, 10 waves
+    case 9: return launch_g3<2, 1, 2, 5, 64, 3, 3>(a, st);        // 128 x 160, 10 waves
+    case 5: return launch_g3<2, 2, 2, 2, 64, 2, 2>(a, st);        // 128 x 128, 4 waves
+    case 6: return launch_g3<2, 1, 1, 4, 64, 3, 2>(a, st);        // 64 x 128, 4 waves
+    case 7: return launch_g3<1, 2, 2, 2, 64, 3, 3>(a, st);        // 64 x 128, 4 waves, three per CU
     case 1: return launch_g3<4, 1, 1, 4, 64, 2>(a, st);           // 128 x 128, 4 waves
     case 2: return launch_g3<2, 2, 2, 4, 64, 2>(a, st);           // 128 x 256, 8 waves
     case 4: return launch_g3<2, 1, 2, 2, 64, 2, 3>(a, st);        // 128 x 64, 4 waves, three per CU

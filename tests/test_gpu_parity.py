@@ -410,7 +410,7 @@ def test_baseline_cfg4_rows_gemm2(gemm2):
     run_config("cfg4", rows=[(0, 256), (17152, 17408)])
 
 
-@pytest.fixture(params=["0", "1", "2", "3", "4"])
+@pytest.fixture(params=["0", "1", "2", "3", "4", "5", "6", "7", "8", "9"])
 def gemm3_tile(request, monkeypatch):
     # every tile configuration of the large-tile kernel
     monkeypatch.setenv("KXW4_GEMM3_TILE", request.param)
