@@ -65,9 +65,18 @@ struct W4Shape {
     static constexpr int AS_BYTES = UPS * BM * 4;        // [group][token] FP32
     static constexpr int AS_OFF = A_BYTES + B_BYTES + S_BYTES;
     static constexpr int STAGE = (AS_OFF + AS_BYTES + 1023) / 1024 * 1024;
-    static constexpr int A_LOADS = A_BYTES / 1024 / NW;  // 1 KB wave loads per wave and stage
-    static constexpr int B_LOADS = BNG / NW;
-    static constexpr int S_LANES = BNG * UPS * 2 / NW;   // 16-byte scale granules per wave
+    // loads per wave and stage, equal for every wave; chunk indices wrap when
+    // the waves do not divide them (a few chunks are then loaded twice)
+    static constexpr int A_CHUNKS = A_BYTES / 1024;
+    static constexpr int A_LOADS = (A_CHUNKS + NW - 1) / NW;
+    static constexpr int B_LOADS = (BNG + NW - 1) / NW;
+    static constexpr int S_TOTAL = BNG * UPS * 2;        // 16-byte scale granules per stage
+    static constexpr int s_lanes() {                     // a divisor of S_TOTAL: no range straddles the wrap
+        int d = (S_TOTAL + NW - 1) / NW;
+        while (S_TOTAL % d) ++d;
+        return d;
+    }
+    static constexpr int S_LANES = s_lanes();
     // 256-byte (one float per lane) wave loads; when the waves outnumber the
     // 64-float rows of the [group][token] block, rows wrap and are loaded by
     // several waves (identical values)
@@ -84,9 +93,8 @@ struct W4Shape {
     static constexpr int lds_bytes() {
         return NST * STAGE > NW * slab_bytes(slab_blocks<NST>()) ? NST * STAGE : NW * slab_bytes(slab_blocks<NST>());
     }
-    static_assert(A_BYTES % (1024 * NW) == 0, "activation tile splits evenly over the waves");
-    static_assert(BNG % NW == 0, "weight tiles split evenly over the waves");
-    static_assert((BNG * UPS * 2) % NW == 0 && S_LANES <= 64, "scale granules split evenly");
+    static_assert(A_BYTES % 1024 == 0, "activation tile in whole 1 KB chunks");
+    static_assert(S_LANES <= 64, "one scale load per wave and stage");
     static_assert((UPS * BM) % 64 == 0, "activation scale rows are whole wave loads");
 };
 
@@ -124,7 +132,7 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void w4a4_kernel(const W4a4Args a
     uint32_t aoffs[S::A_LOADS];
 #pragma unroll
     for (int i = 0; i < S::A_LOADS; ++i) {
-        const int p = (wave + NW * i) * 64 + lane;            // 16-byte granule this lane fills
+        const int p = ((wave + NW * i) % S::A_CHUNKS) * 64 + lane;   // 16-byte granule this lane fills
         const int t = p >> 2;                                 // token of the tile
         const int c = (p & 3) ^ ((t >> 2) & 3);               // source chunk stored at slot p & 3
         aoffs[i] = (uint32_t)min(t0 + t, T - 1) * 64 + c * 16;   // rows past T: never stored
@@ -132,12 +140,12 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void w4a4_kernel(const W4a4Args a
     uint32_t boffs[S::B_LOADS];
 #pragma unroll
     for (int i = 0; i < S::B_LOADS; ++i) {
-        const int rg = min(rg0 + wave + NW * i, RG - 1);      // row-groups past M: never stored
+        const int rg = min(rg0 + (wave + NW * i) % BNG, RG - 1);   // row-groups past M: never stored
         boffs[i] = (uint32_t)rg * NT * kTileBytes + lane * 16;
     }
     uint32_t soff;
     {
-        const int gi = wave * S::S_LANES + min(lane, S::S_LANES - 1);
+        const int gi = (wave * S::S_LANES + min(lane, S::S_LANES - 1)) % S::S_TOTAL;
         const int j = gi / (2 * UPS), u = (gi >> 1) % UPS, half = gi & 1;
         const int rg = min(rg0 + j, RG - 1);
         soff = ((uint32_t)rg * G + u) * 16 + half * 8;
@@ -156,16 +164,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void w4a4_kernel(const W4a4Args a
 #pragma unroll
         for (int i = 0; i < S::A_LOADS; ++i)
             __builtin_amdgcn_global_load_lds((const void *)(ak + aoffs[i]),
-                                             KXW4_W4_LDS(base + (wave + NW * i) * 1024), 16, 0, 0);
+                                             KXW4_W4_LDS(base + ((wave + NW * i) % S::A_CHUNKS) * 1024), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < S::B_LOADS; ++i)
             __builtin_amdgcn_global_load_lds((const void *)(wk + boffs[i]),
-                                             KXW4_W4_LDS(base + A_BYTES + (wave + NW * i) * 1024), 16, 0, 0);
+                                             KXW4_W4_LDS(base + A_BYTES + ((wave + NW * i) % BNG) * 1024), 16, 0, 0);
         // lanes past the wave's granules are masked off; the load still
         // counts once in vmcnt
         if (lane < S::S_LANES)
             __builtin_amdgcn_global_load_lds((const void *)(a.scales + (size_t)kb * UPS * 16 + soff),
-                                             KXW4_W4_LDS(base + A_BYTES + B_BYTES + wave * S::S_LANES * 16),
+                                             KXW4_W4_LDS(base + A_BYTES + B_BYTES + (wave * S::S_LANES) % S::S_TOTAL * 16),
                                              16, 0, 0);
 #pragma unroll
         for (int i = 0; i < S::AS_LOADS; ++i)
@@ -396,10 +404,15 @@ static int launch_w4(W4a4Args &a, hipStream_t st) {
 }
 
 int launch_w4a4(W4a4Args &a, hipStream_t st) {
-    // KXW4_W4A4_TILE=0..2 picks one configuration (tests and tuning)
+    // Default 128 x 64 (three work-groups per CU). The 64 x 160 tile (10
+    // waves, one work-group per CU) balances the cfg2 M=512 grid better but
+    // measures slower (207 vs 192 us): with one token block per wave the
+    // zero-point weight unpack is no longer shared. KXW4_W4A4_TILE=0..3 picks
+    // one configuration (tests, tuning).
     const char *cfg = getenv("KXW4_W4A4_TILE");
     const int sel = cfg ? atoi(cfg) : 0;
     switch (sel) {
+    case 3: return launch_w4<1, 1, 2, 5, 3, 3>(a, st);      // 64 tokens x 160 rows, 10 waves
     case 1: return launch_w4<2, 1, 2, 4, 3, 2>(a, st);      // 128 tokens x 128 rows, 8 waves
     case 2: return launch_w4<1, 2, 2, 2, 3, 2>(a, st);      // 64 tokens x 128 rows, 4 waves
     default: return launch_w4<2, 1, 2, 2, 3, 2>(a, st);     // 128 tokens x 64 rows, 4 waves
