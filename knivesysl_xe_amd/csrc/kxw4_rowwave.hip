@@ -152,8 +152,30 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
     __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * TB));
-    const bool ref_block = a.block == 32, zp = a.scale_enc == 1 && !K16;
-    if (MODE != 0) {
+    // W8 has no zero points and K16 folds them into the weight bytes
+    const bool ref_block = a.block == 32, zp = WF == kWfW4 && a.scale_enc == 1;
+    if (MODE != 0 && UNIT == 32 && ref_block) {
+        // per-unit (= per-K32) activation scale and zero-point code sum,
+        // [Nu][16 token slots]; each thread reads four consecutive units of
+        // one token row with one 16-byte load (rows are K/32 entries, a
+        // multiple of 4) and scatters them into the token-minor table
+        const int n4 = Nu / 4;
+        for (int x = tid; x < 16 * n4; x += nthreads) {
+            const int slot = x / n4, u = 4 * (x - slot * n4);
+            const size_t src = (size_t)min(slot, T - 1) * Nu + u;
+            const float4 sc = *reinterpret_cast<const float4 *>(a.ascale + src);
+            int4 sm = {0, 0, 0, 0};
+            if (zp) sm = *reinterpret_cast<const int4 *>(a.asum + src);
+            Asc[u * 16 + slot] = sc.x;
+            Asc[(u + 1) * 16 + slot] = sc.y;
+            Asc[(u + 2) * 16 + slot] = sc.z;
+            Asc[(u + 3) * 16 + slot] = sc.w;
+            Zs[u * 16 + slot] = sm.x;
+            Zs[(u + 1) * 16 + slot] = sm.y;
+            Zs[(u + 2) * 16 + slot] = sm.z;
+            Zs[(u + 3) * 16 + slot] = sm.w;
+        }
+    } else if (MODE != 0) {
         // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
         for (int x = tid; x < Nu * 16; x += nthreads) {
             const int u = x >> 4, t = min(x & 15, T - 1);
@@ -268,7 +290,8 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                         } else {
                             const float w = half_bits_to_float(zp ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
                             const int z = sext4(sv);
-                            const v4i zv = *reinterpret_cast<const v4i *>(Zs + u * 16 + 4 * g4);
+                            v4i zv = {0, 0, 0, 0};
+                            if (WF == kWfW4) zv = *reinterpret_cast<const v4i *>(Zs + u * 16 + 4 * g4);
                             const float4 av = *reinterpret_cast<const float4 *>(in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4);
                             const float avr[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
