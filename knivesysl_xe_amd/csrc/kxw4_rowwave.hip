@@ -7,9 +7,10 @@
 // chain in registers: the int8 MFMA leaves row n of tokens 4*(l/16)+r in
 // register r of lane l for every unit, so a lane's four accumulators are four
 // of the reference's chains, fed unit by unit in order. The waves of one
-// row-group take consecutive splits (a work-group holds 8 / min(S, 8)
-// row-groups); with S > 1 the split partials meet in LDS and one wave adds
-// them in split order starting from 0.0f.
+// row-group take consecutive splits (a work-group holds one or more
+// row-groups of min(S, 8) waves each, at most 16 waves); with S > 1 the split
+// partials meet in LDS and one wave adds them in split order starting from
+// 0.0f.
 //
 // The activations (T x K int8) and the work-group's FP16 scales are staged
 // into LDS once per work-group with direct global->LDS loads, so the
@@ -40,7 +41,11 @@
 
 namespace kxw4 {
 
-constexpr int kRwWaves = 8;                 // waves per work-group by default
+// wave budget of a plain work-group (wpw / wrg row-groups): 10 measured best
+// at the cfg1 shape (5 row-groups of 2 splits: 20.7 us against 23.2 us at 8
+// waves and 21.3 us for the balanced plan)
+constexpr int kRwWaves = 10;
+constexpr int kRwSplitWaves = 8;            // most waves that share one row-group's splits
 constexpr int kRwMaxWaves = 16;
 constexpr size_t kRwLdsMax = 160 * 1024;
 
@@ -85,9 +90,13 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     const int pitch = K + 16;                                 // padded activation row
     int8_t *Act = reinterpret_cast<int8_t *>(smem);
     uint16_t *Sc = reinterpret_cast<uint16_t *>(smem + (size_t)T * pitch);
+    // the zero-point code-sum table exists only for FP16|zp W4 weights (W8
+    // has no zero points and K16 folds them into the weight bytes), so the
+    // other formats ask for less LDS
+    const bool zp = WF == kWfW4 && a.scale_enc == 1;
     float *Asc = reinterpret_cast<float *>(Sc + R * G * 16);
     int *Zs = reinterpret_cast<int *>(Asc + (MODE != 0 ? Nu * 16 : 0));
-    float *Part = reinterpret_cast<float *>(Zs + (MODE != 0 ? Nu * 16 : 0));
+    float *Part = reinterpret_cast<float *>(Zs + (MODE != 0 && zp ? Nu * 16 : 0));
     // 16 zero words: the scale (and activation scale) read of a padded
     // position, so its chain step fma(p, 0, acc) leaves acc unchanged
     // (p is a finite integer and a chain that starts at +0 never holds -0)
@@ -152,8 +161,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
     __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * TB));
-    // W8 has no zero points and K16 folds them into the weight bytes
-    const bool ref_block = a.block == 32, zp = WF == kWfW4 && a.scale_enc == 1;
+    const bool ref_block = a.block == 32;
     if (MODE != 0 && UNIT == 32 && ref_block) {
         // per-unit (= per-K32) activation scale and zero-point code sum,
         // [Nu][16 token slots]; each thread reads four consecutive units of
@@ -164,27 +172,29 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
             const int slot = x / n4, u = 4 * (x - slot * n4);
             const size_t src = (size_t)min(slot, T - 1) * Nu + u;
             const float4 sc = *reinterpret_cast<const float4 *>(a.ascale + src);
-            int4 sm = {0, 0, 0, 0};
-            if (zp) sm = *reinterpret_cast<const int4 *>(a.asum + src);
             Asc[u * 16 + slot] = sc.x;
             Asc[(u + 1) * 16 + slot] = sc.y;
             Asc[(u + 2) * 16 + slot] = sc.z;
             Asc[(u + 3) * 16 + slot] = sc.w;
-            Zs[u * 16 + slot] = sm.x;
-            Zs[(u + 1) * 16 + slot] = sm.y;
-            Zs[(u + 2) * 16 + slot] = sm.z;
-            Zs[(u + 3) * 16 + slot] = sm.w;
+            if (zp) {
+                const int4 sm = *reinterpret_cast<const int4 *>(a.asum + src);
+                Zs[u * 16 + slot] = sm.x;
+                Zs[(u + 1) * 16 + slot] = sm.y;
+                Zs[(u + 2) * 16 + slot] = sm.z;
+                Zs[(u + 3) * 16 + slot] = sm.w;
+            }
         }
     } else if (MODE != 0) {
         // per-unit activation scale and zero-point code sum, [Nu][16 tokens]
         for (int x = tid; x < Nu * 16; x += nthreads) {
             const int u = x >> 4, t = min(x & 15, T - 1);
             Asc[x] = ref_block ? a.ascale[(size_t)t * (K / 32) + u] : 1.0f;
-            int sm = 0;
-            if (zp)
+            if (zp) {
+                int sm = 0;
                 for (int q = (u * UNIT) / 32; q < ((u + 1) * UNIT) / 32; ++q)
                     sm += a.asum[(size_t)t * (K / 32) + q];
-            Zs[x] = sm;
+                Zs[x] = sm;
+            }
         }
     }
     if (tid < 16) Zero[tid] = 0.0f;
@@ -291,7 +301,9 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                             const float w = half_bits_to_float(zp ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
                             const int z = sext4(sv);
                             v4i zv = {0, 0, 0, 0};
-                            if (WF == kWfW4) zv = *reinterpret_cast<const v4i *>(Zs + u * 16 + 4 * g4);
+                            if (WF == kWfW4)
+                                zv = *reinterpret_cast<const v4i *>(zp ? Zs + u * 16 + 4 * g4
+                                                                       : reinterpret_cast<const int *>(Zero) + 4 * g4);
                             const float4 av = *reinterpret_cast<const float4 *>(in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4);
                             const float avr[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
@@ -401,12 +413,17 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     const int unit = a.block == 32 ? 32 : a.group;
     const int nu = a.K / unit, g = a.K / a.group;
     const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
-    // Default shape: 8 waves per work-group, 8 / wrg row-groups each. When
-    // that leaves a partial last round of work-groups over the CUs (the CUs
-    // holding one more work-group finish last), the weights' row-groups are
-    // instead dealt to exactly k work-groups per CU, each owning
-    // ceil(row-groups / work-groups) row-groups at most, and the LDS request
-    // keeps a (k+1)-th work-group off every CU.
+    // Plain shape: a budget of kRwWaves waves per work-group, wpw / wrg
+    // row-groups each. When the LDS holds only one such work-group per CU
+    // (large scale tables: W8's per-K32 scales, 16 token rows), the CU's only
+    // memory parallelism is that work-group, so it takes 16 waves instead.
+    // Otherwise, when the plain shape leaves a partial last round of
+    // work-groups over the CUs (the CUs holding one more work-group finish
+    // last), the weights' row-groups are instead dealt to exactly k
+    // work-groups per CU, each owning ceil(row-groups / work-groups)
+    // row-groups at most, and the LDS request keeps a (k+1)-th work-group off
+    // every CU; that plan is kept only when it lowers the most row-groups a
+    // CU streams.
     int rg_total = 0, wrg_max = 1, tiles = 0;
     for (int i = 0; i < a.count; ++i) {
         DecodeWeight &w = a.w[i];
@@ -414,51 +431,68 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         for (int s = 1; s < a.seg_count; ++s)
             if (w.seg_split[s] != S) return 1;
         if (S < 1 || S > 16 || (S & (S - 1))) return 1;
-        w.wrg = std::min(S, kRwWaves);
+        w.wrg = std::min(S, kRwSplitWaves);
         wrg_max = std::max(wrg_max, w.wrg);
         rg_total += w.M / 16;
         tiles = std::max(tiles, (a.K / kTileK + S - 1) / S);
     }
-    int wg_default = 0;
-    for (int i = 0; i < a.count; ++i) wg_default += (a.w[i].M / 16 + kRwWaves / a.w[i].wrg - 1) / (kRwWaves / a.w[i].wrg);
     const int cus = device_cus();
-    const int k = wg_default / cus;
-    bool balanced = k >= 1 && wg_default % cus != 0 && !getenv("KXW4_ROWWAVE_DEFAULT_GRID");
-    int wg = 0, waves = kRwWaves, rmax = 1, part = 0;
-    auto plan = [&](bool bal) {
+    // KXW4_ROWWAVE_RPW=r: r row-groups per work-group (r * min(S, 8) waves)
+    const char *rpe = getenv("KXW4_ROWWAVE_RPW");
+    const int rpw = rpe ? atoi(rpe) : 0;
+    if (rpw < 0 || rpw * wrg_max > kRwMaxWaves) return 1;
+    int wpw = rpw ? rpw * wrg_max : kRwWaves;
+    int wg = 0, waves = 0, rmax = 1, part = 0;
+    // k > 0: k work-groups per CU over all weights; k = 0: the plain shape
+    auto plan = [&](int k) {
         wg = 0;
-        waves = bal ? 0 : kRwWaves;
+        waves = 0;
         rmax = 1;
         part = 0;
         for (int i = 0; i < a.count; ++i) {
             DecodeWeight &w = a.w[i];
             const int RG = w.M / 16, S = w.seg_split[0];
-            int n = bal ? (int)(((long long)k * cus * RG + rg_total / 2) / rg_total)
-                        : (RG + kRwWaves / w.wrg - 1) / (kRwWaves / w.wrg);
+            const int per = std::max(1, wpw / w.wrg);
+            int n = k ? (int)(((long long)k * cus * RG + rg_total / 2) / rg_total) : (RG + per - 1) / per;
             n = std::max(1, std::min(n, RG));
             const int R = (RG + n - 1) / n;
             w.wg_begin = wg;
             w.wg_count = n;
             wg += n;
             rmax = std::max(rmax, R);
-            if (bal) waves = std::max(waves, R * w.wrg);
+            waves = std::max(waves, (k ? R : per) * w.wrg);
             if (S > 1) part = std::max(part, R * (S - 1));
         }
     };
-    if (balanced) {
-        // keep the balanced plan only when it lowers the most row-groups a
-        // CU streams
-        plan(false);
-        const int load_default = (wg_default + cus - 1) / cus * rmax;
-        plan(true);
-        if (waves > kRwMaxWaves || k * rmax >= load_default) balanced = false;
+    // the work-group's LDS: padded activation rows, its row-groups' scales,
+    // the per-unit activation scales and, for FP16|zp W4 weights (the
+    // kernel's zp), the zero-point code sums, the split partials
+    const bool zp_table = !a.w8 && a.group != 16 && a.scale_enc == 1;
+    auto lds_bytes = [&]() {
+        return (size_t)a.T * (a.K + 16) + (size_t)rmax * g * 32 +
+               (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
+    };
+    plan(0);
+    int k = 0;
+    if (!rpw && 2 * lds_bytes() > kRwLdsMax) {
+        wpw = kRwMaxWaves;
+        plan(0);
+        if (lds_bytes() > kRwLdsMax) {          // the larger tables do not fit
+            wpw = kRwWaves;
+            plan(0);
+        }
+    } else if (!rpw && !getenv("KXW4_ROWWAVE_DEFAULT_GRID") && wg >= cus && wg % cus != 0) {
+        const int load_plain = (wg + cus - 1) / cus * rmax;
+        k = wg / cus;
+        plan(k);
+        if (waves > kRwMaxWaves || k * rmax >= load_plain) {
+            k = 0;
+            plan(0);
+        }
     }
-    if (!balanced) plan(false);
-    const size_t act = (size_t)a.T * (a.K + 16);
-    const size_t scales = (size_t)rmax * g * 32;
-    size_t lds = act + scales + (mode != 0 ? (size_t)2 * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
+    size_t lds = lds_bytes();
     if (lds > kRwLdsMax) return 1;
-    if (balanced) lds = std::max(lds, (size_t)160 * 1024 / (k + 1) + 1024);
+    if (k) lds = std::max(lds, (size_t)160 * 1024 / (k + 1) + 1024);
     const dim3 block(64 * waves);
     const dim3 grid(wg);
     // KXW4_ROWWAVE_PF=8 takes the deeper ring (measured slower: more loads in
