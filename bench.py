@@ -319,6 +319,50 @@ def calibration_copy(mib):
     log(f"calibration copy: 3 x {mib} MiB")
 
 
+def machine_probes(head_bytes):
+    """Measured ceilings, the MI355X counterpart of the reference's
+    xpu/probe/dpas_probe.cpp (DPAS rates with all-ones operands, pure read;
+    xpu/PROBE_RESULTS.md:8-33): the int8 MFMA rate of both MFMA shapes, with
+    the all-ones check, and the pure HBM read rate over a 2 GiB buffer and
+    over slices of the headline's byte count rotated through it."""
+    import torch
+    from knivesysl_xe_amd import ops
+    sink = torch.empty(ops.PROBE_SINK_WORDS, dtype=torch.int32, device="cuda")
+    out = {}
+
+    def timed(fn, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    for shape, name, k, iters in ((0, "mfma_i8_32x32x32", 32, 20000), (1, "mfma_i8_16x16x64", 64, 40000)):
+        ops.probe_mfma_i8(shape, 100, sink)
+        res = {}
+        secs = timed(lambda _i: res.update(zip(("n", "ops"), ops.probe_mfma_i8(shape, iters, sink))), 3)
+        out[f"{name}_TOPS"] = res["ops"] / secs / 1e12
+        out[f"{name}_check"] = bool((sink[:res["n"]] == iters * k).all().item())
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    n = (head_bytes + 4095) // 4096 * 4096
+    slices = [buf[i * n:(i + 1) * n] for i in range(buf.numel() // n)]
+    best_full, best_head = (0.0, -1), (0.0, -1)
+    for shape in range(ops.probe_read_shapes()):
+        ops.probe_read(buf, sink, shape)
+        secs = timed(lambda _i: ops.probe_read(buf, sink, shape), 5)
+        best_full = max(best_full, (buf.numel() / secs / 1e9, shape))
+        secs = timed(lambda i: ops.probe_read(slices[i % len(slices)], sink, shape), 2 * len(slices))
+        best_head = max(best_head, (n / secs / 1e9, shape))
+    out["hbm_read_2GiB_GBps"], out["hbm_read_2GiB_shape"] = best_full
+    out["hbm_read_headline_bytes_GBps"], out["hbm_read_headline_bytes_shape"] = best_head
+    out["read_sample"] = (f"fastest of {ops.probe_read_shapes()} launch shapes; 2 GiB: 5 sweeps; headline "
+                          f"bytes: {len(slices)} slices of {n} bytes rotated through 2 GiB, back-to-back launches")
+    del buf
+    return out
+
+
 def read_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any:
     fetch_kib * fetch_cal + write_kib * write_cal, where each factor is the
@@ -350,6 +394,7 @@ def main():
     ap.add_argument("--w4a4", default="cfg2_m512",
                     help="K64 configs to also run through the W4A4 GEMM ('' for none)")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
+    ap.add_argument("--no-probes", action="store_true", help="skip the MFMA / HBM read probes")
     ap.add_argument("--extra-steps", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
@@ -388,6 +433,13 @@ def main():
         e = extra["lm_head_w8a8"] = measure_w8a8(20, 3, args.eager)
         log(f"lm_head_w8a8: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, frac {e['roofline_frac']:.3f}, "
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
+    probes = None
+    if not args.no_probes:
+        probes = machine_probes(int(r["bytes"]))
+        log(f"probes: MFMA i8 32x32x32 {probes['mfma_i8_32x32x32_TOPS']:.0f} TOPS "
+            f"(check {probes['mfma_i8_32x32x32_check']}), 16x16x64 {probes['mfma_i8_16x16x64_TOPS']:.0f} TOPS "
+            f"(check {probes['mfma_i8_16x16x64_check']}); read {probes['hbm_read_2GiB_GBps']:.0f} GB/s (2 GiB), "
+            f"{probes['hbm_read_headline_bytes_GBps']:.0f} GB/s (headline bytes)")
     if args.copy_mib:
         calibration_copy(args.copy_mib)
     log("cpu baseline (oracle on host cores)")
@@ -415,6 +467,9 @@ def main():
                      "traffic": read_traffic("cfg1")},
         "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()},
         "bit_exact_vs_oracle": r["bit_exact_vs_oracle_rows0_512"],
+        "probes": None if probes is None else dict(
+            {k: (round(v, 2) if isinstance(v, float) else v) for k, v in probes.items()},
+            headline_frac_of_read_probe=round(r["GBps"] / probes["hbm_read_headline_bytes_GBps"], 4)),
         "quantize_us": round(r["quantize_us"], 2),
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in extra.items()},

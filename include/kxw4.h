@@ -269,6 +269,25 @@ int kxw4_tqf_find(const kxw4_tqf_t *t, const char *name);
 int kxw4_tqf_load_qmma(const kxw4_tqf_t *t, int index, int mode,
                        uint8_t *out_codes, uint16_t *out_scales, void *stream);
 
+/* Machine probes (xpu/probe/dpas_probe.cpp, results xpu/PROBE_RESULTS.md:
+ * 8-33: DPAS rates with all-ones operands, pure-read bandwidth), the ceilings
+ * the roofline fractions are read against besides the published peaks. They
+ * enqueue one kernel on `stream`; the caller times it.
+ * kxw4_probe_mfma_i8: shape 0 = v_mfma_i32_32x32x32_i8, 1 = _16x16x64_i8,
+ * four independent all-ones chains per wave; each wave writes iters * K to
+ * its sink word when every accumulator holds exactly that, else -1. *ops
+ * receives the launch's integer operation count. kxw4_probe_read: a
+ * grid-stride read of `bytes` (16-byte aligned, multiple of 16) in launch
+ * shape `shape` (0 .. kxw4_probe_read_shapes() - 1: work-groups per CU,
+ * threads, loads in flight per lane), one XOR checksum word per wave. Both
+ * return the number of sink words written (sink_words must be at least
+ * that: 64K words cover any GPU), or -1 / -2 (sink too small) / -6. */
+int kxw4_probe_mfma_i8(int shape, int iters, int32_t *sink, int sink_words, double *ops,
+                       void *stream);
+int kxw4_probe_read(const void *buf, size_t bytes, int shape, uint32_t *sink, int sink_words,
+                    void *stream);
+int kxw4_probe_read_shapes(void);
+
 /* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
  * else group), from the same unpack and MFMA code as the projections. */
 int kxw4_partials(const kxw4_weight_t *w, const kxw4_act_t *a, int32_t *P,

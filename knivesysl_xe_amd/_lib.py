@@ -67,6 +67,9 @@ SIGNATURES = {
     "kxw4_tqf_tensor": (I, [P, I, C.POINTER(TqfTensor)]),
     "kxw4_tqf_find": (I, [P, C.c_char_p]),
     "kxw4_tqf_load_qmma": (I, [P, I, I, P, P, P]),
+    "kxw4_probe_mfma_i8": (I, [I, I, P, I, C.POINTER(C.c_double), P]),
+    "kxw4_probe_read": (I, [P, C.c_size_t, I, P, I, P]),
+    "kxw4_probe_read_shapes": (I, []),
     "kxw4_partials": (I, [WP, AP, P, P]),
 }
 

@@ -417,3 +417,31 @@ def gemv_splits(groups: int) -> int:
 
 def gemm_splits(rgroups: int, tgroups: int, ktiles: int, forced: int = 0) -> int:
     return lib().kxw4_gemm_splits(rgroups, tgroups, ktiles, forced)
+
+
+PROBE_SINK_WORDS = 1 << 16
+
+
+def probe_mfma_i8(shape: int, iters: int, sink: torch.Tensor) -> tuple:
+    """Enqueue the int8 MFMA rate probe (shape 0 = 32x32x32, 1 = 16x16x64) on
+    the current stream; returns (sink words written, operation count). Each
+    word is iters * K when its wave's accumulators all hold exactly that."""
+    ops_count = C.c_double()
+    n = lib().kxw4_probe_mfma_i8(shape, iters, _ptr(sink), sink.numel(), C.byref(ops_count), _stream())
+    if n < 0:
+        raise _lib.KxError("kxw4_probe_mfma_i8", n)
+    return n, ops_count.value
+
+
+def probe_read_shapes() -> int:
+    return lib().kxw4_probe_read_shapes()
+
+
+def probe_read(buf: torch.Tensor, sink: torch.Tensor, shape: int = 0) -> int:
+    """Enqueue the pure-read probe over all of `buf` on the current stream in
+    launch shape `shape`; returns the number of checksum words written."""
+    n = lib().kxw4_probe_read(_ptr(buf), buf.numel() * buf.element_size(), shape, _ptr(sink), sink.numel(),
+                              _stream())
+    if n < 0:
+        raise _lib.KxError("kxw4_probe_read", n)
+    return n

@@ -338,6 +338,15 @@ def test_baseline_config_persist(name, persist):
     run_config(name)
 
 
+@pytest.mark.parametrize("rpw", ["1", "3", "4", "8"])
+def test_cfg1_rowwave_shapes(rpw, monkeypatch):
+    # the row-wave kernel's work-group shape changes only who streams which
+    # row-group: every shape gives the same bits (4 = the partial-round shape
+    # that the launcher replaces by its balanced plan when left to itself)
+    monkeypatch.setenv("KXW4_ROWWAVE_RPW", rpw)
+    run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
+
+
 @pytest.mark.parametrize("rows,K,T,group,block,enc,variant,forced", [
     # fewer chains than CUs: row-groups spread over several work-groups
     ([64], 4096, 1, 128, 0, 0, "gemv", 0),
