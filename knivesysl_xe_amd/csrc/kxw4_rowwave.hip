@@ -25,7 +25,9 @@
 // 771-844, 1578-1629): 2 KB int8 tiles, two 16-byte loads per lane and tile,
 // used as the K32 MFMA operand without an unpack; the MFMA result is the unit
 // partial itself (no factor 16) and the chain is the reference mode's with
-// zero point 0.
+// zero point 0. The per-K32 scales are not staged (they would take 5 KB of
+// LDS per row-group): one 2-byte load per lane and tile rides in the ring,
+// and four lane shuffles hand each lane its row's four unit scales.
 //
 // K16 (the K16 tier, x_gemv_w4a8_core_k16, kernels_dpas.cpp:683-760): GEMV
 // only, FP16|zp scales per K16 half. A K32 unit's lane groups 0-1 hold half 0
@@ -94,7 +96,8 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     // has no zero points and K16 folds them into the weight bytes), so the
     // other formats ask for less LDS
     const bool zp = WF == kWfW4 && a.scale_enc == 1;
-    float *Asc = reinterpret_cast<float *>(Sc + R * G * 16);
+    // W8 scales are not staged: they stream through the ring (below)
+    float *Asc = reinterpret_cast<float *>(Sc + (W8 ? 0 : R * G * 16));
     int *Zs = reinterpret_cast<int *>(Asc + (MODE != 0 ? Nu * 16 : 0));
     float *Part = reinterpret_cast<float *>(Zs + (MODE != 0 && zp ? Nu * 16 : 0));
     // 16 zero words: the scale (and activation scale) read of a padded
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     // (the last chunk of a row is padding), then the work-group's scales.
     const int kc = K / 16;
     const int act_chunks = T * (kc + 1);
-    const int total = act_chunks + nrg * G * 2;
+    const int total = act_chunks + (W8 ? 0 : nrg * G * 2);
     for (int c0 = wave * 64; c0 < total; c0 += nthreads) {
         const int x = c0 + lane;
         if (x < total) {
@@ -148,19 +151,27 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
     int kt0 = u0 / UPS, ntw = (u1 + UPS - 1) / UPS - kt0;
     const v4u *wrow = reinterpret_cast<const v4u *>(W.codes + (size_t)rg * NT * kTileBytes * TB) + lane;
     v4u ring[PF][TB];
+    // W8: the tile's FP16 scales ride in the ring, one per lane: lane n+16j
+    // holds unit j's scale of row n (the tile's 128 bytes of the [rg][G][16]
+    // table); the chain spreads them to the row's lanes with shuffles
+    uint32_t sring[W8 ? PF : 1];
+    const uint16_t *wsc = W.scales + ((size_t)rg * G + g4) * 16 + n;
     // tile i of the current split; an empty split (more splits than units)
     // or an idle wave reads a valid tile it never uses
-    auto load = [&](int i, v4u (&dst)[TB]) {
-        const size_t t = (size_t)min(kt0 + max(i, 0), NT - 1) * (kTileBytes * TB / 16);
+    auto load = [&](int i, int p) {
+        const int kt = min(kt0 + max(i, 0), NT - 1);
+        const size_t t = (size_t)kt * (kTileBytes * TB / 16);
 #pragma unroll
-        for (int h = 0; h < TB; ++h) dst[h] = wrow[t + 64 * h];
+        for (int h = 0; h < TB; ++h) ring[p][h] = wrow[t + 64 * h];
+        if constexpr (W8) sring[p] = wsc[(size_t)kt * (kTileK / 32) * 16];
     };
+    constexpr int LPT = TB + (W8 ? 1 : 0);         // loads per tile
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), ring[p]);
+    for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), p);
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * TB));
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * LPT));
     const bool ref_block = a.block == 32;
     if (MODE != 0 && UNIT == 32 && ref_block) {
         // per-unit (= per-K32) activation scale and zero-point code sum,
@@ -217,7 +228,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                 kt0 = u0 / UPS;
                 ntw = (u1 + UPS - 1) / UPS - kt0;
 #pragma unroll
-                for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), ring[p]);
+                for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), p);
             }
             float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -235,6 +246,12 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                     const v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
                     const v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
                     const v4u wd = ring[p][0];
+                    // W8: unit j's scale of this lane's row, from lane n + 16j
+                    uint32_t s8[W8 ? 4 : 1];
+                    if constexpr (W8) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) s8[j] = (uint32_t)__shfl((int)sring[p], n + 16 * j);
+                    }
 #pragma unroll
                     for (int j = 0; j < UPS; ++j) {
                         const int u = kb * UPS + j;
@@ -283,7 +300,9 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                         }
                         // MODE 0 has unit == group, so unit u reads scale u
                         const uint16_t *sp = MODE == 0 ? &sr[(p * UPS + j) * 16] : &sbase[(u >> gsh) * 16];
-                        const uint32_t sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
+                        uint32_t sv;
+                        if constexpr (W8) sv = in ? s8[W8 ? j : 0] : 0u;
+                        else sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
                         // GEMV: units at odd offsets from the split start feed the
                         // second accumulator. With an even ring and an even number
                         // of units per tile the parity is fixed by p (whole-tile
@@ -319,7 +338,7 @@ __global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeA
                             }
                         }
                     }
-                    load(min(i + PF, ntw - 1), ring[p]);
+                    load(min(i + PF, ntw - 1), p);
                     // keep each slot's unpack behind the previous slot's load, so
                     // the wait before it covers only that slot
                     __builtin_amdgcn_sched_barrier(0);
@@ -415,15 +434,17 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
     // Plain shape: a budget of kRwWaves waves per work-group, wpw / wrg
     // row-groups each. When the LDS holds only one such work-group per CU
-    // (large scale tables: W8's per-K32 scales, 16 token rows), the CU's only
-    // memory parallelism is that work-group, so it takes 16 waves instead.
-    // Otherwise, when the plain shape leaves a partial last round of
-    // work-groups over the CUs (the CUs holding one more work-group finish
-    // last), the weights' row-groups are instead dealt to exactly k
-    // work-groups per CU, each owning ceil(row-groups / work-groups)
-    // row-groups at most, and the LDS request keeps a (k+1)-th work-group off
-    // every CU; that plan is kept only when it lowers the most row-groups a
-    // CU streams.
+    // (large tables: 16 token rows, long K), the CU's only memory parallelism
+    // is that work-group, so it takes 16 waves instead; so do weights that
+    // need four or more rounds of work-groups per CU (lm_head-sized), where
+    // fewer, larger work-groups stage the activations fewer times (W8A8
+    // lm_head T=8: 311 -> 271 us). Otherwise, when the plain shape leaves a
+    // partial last round of work-groups over the CUs (the CUs holding one
+    // more work-group finish last), the weights' row-groups are instead
+    // dealt to exactly k work-groups per CU, each owning ceil(row-groups /
+    // work-groups) row-groups at most, and the LDS request keeps a (k+1)-th
+    // work-group off every CU; that plan is kept only when it lowers the
+    // most row-groups a CU streams.
     int rg_total = 0, wrg_max = 1, tiles = 0;
     for (int i = 0; i < a.count; ++i) {
         DecodeWeight &w = a.w[i];
@@ -469,12 +490,12 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // kernel's zp), the zero-point code sums, the split partials
     const bool zp_table = !a.w8 && a.group != 16 && a.scale_enc == 1;
     auto lds_bytes = [&]() {
-        return (size_t)a.T * (a.K + 16) + (size_t)rmax * g * 32 +
+        return (size_t)a.T * (a.K + 16) + (a.w8 ? 0 : (size_t)rmax * g * 32) +
                (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) + (size_t)part * 256 * 4 + 64;
     };
     plan(0);
     int k = 0;
-    if (!rpw && 2 * lds_bytes() > kRwLdsMax) {
+    if (!rpw && (2 * lds_bytes() > kRwLdsMax || wg >= 4 * cus)) {
         wpw = kRwMaxWaves;
         plan(0);
         if (lds_bytes() > kRwLdsMax) {          // the larger tables do not fit
