@@ -49,12 +49,15 @@ namespace kxw4 {
 constexpr int kRwWaves = 10;
 constexpr int kRwSplitWaves = 8;            // most waves that share one row-group's splits
 constexpr int kRwMaxWaves = 16;
+// K16 work-groups stay at 8 waves, so the kernel may keep 256 registers per
+// lane (its two masked half MFMAs and scale folds per unit spill at 128)
+constexpr int kRwK16Waves = 8;
 constexpr size_t kRwLdsMax = 160 * 1024;
 
 enum { kWfW4 = 0, kWfW8 = 1, kWfK16 = 2 };     // weight format of a row-wave instance
 
 template <int TT, int UNIT, int MODE, bool ALT2, int PF, int WF>
-__global__ __launch_bounds__(64 * kRwMaxWaves) void rowwave_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(64 * (WF == kWfK16 ? kRwK16Waves : kRwMaxWaves)) void rowwave_kernel(const DecodeArgs a) {
     constexpr int UPS = kTileK / UNIT;
     constexpr bool W8 = WF == kWfW8, K16 = WF == kWfK16;
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
@@ -461,8 +464,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // KXW4_ROWWAVE_RPW=r: r row-groups per work-group (r * min(S, 8) waves)
     const char *rpe = getenv("KXW4_ROWWAVE_RPW");
     const int rpw = rpe ? atoi(rpe) : 0;
-    if (rpw < 0 || rpw * wrg_max > kRwMaxWaves) return 1;
-    int wpw = rpw ? rpw * wrg_max : kRwWaves;
+    const int max_waves = a.group == 16 ? kRwK16Waves : kRwMaxWaves;
+    if (rpw < 0 || rpw * wrg_max > max_waves) return 1;
+    int wpw = rpw ? rpw * wrg_max : std::min(kRwWaves, max_waves);
     int wg = 0, waves = 0, rmax = 1, part = 0;
     // k > 0: k work-groups per CU over all weights; k = 0: the plain shape
     auto plan = [&](int k) {
@@ -496,17 +500,17 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     plan(0);
     int k = 0;
     if (!rpw && (2 * lds_bytes() > kRwLdsMax || wg >= 4 * cus)) {
-        wpw = kRwMaxWaves;
+        wpw = max_waves;
         plan(0);
         if (lds_bytes() > kRwLdsMax) {          // the larger tables do not fit
-            wpw = kRwWaves;
+            wpw = std::min(kRwWaves, max_waves);
             plan(0);
         }
     } else if (!rpw && !getenv("KXW4_ROWWAVE_DEFAULT_GRID") && wg >= cus && wg % cus != 0) {
         const int load_plain = (wg + cus - 1) / cus * rmax;
         k = wg / cus;
         plan(k);
-        if (waves > kRwMaxWaves || k * rmax >= load_plain) {
+        if (waves > max_waves || k * rmax >= load_plain) {
             k = 0;
             plan(0);
         }
