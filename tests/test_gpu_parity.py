@@ -328,6 +328,23 @@ def persist(monkeypatch):
     monkeypatch.setenv("KXW4_DECODE_KERNEL", "persist")
 
 
+@pytest.fixture
+def rowwave(monkeypatch):
+    # per-token shapes with at most 8 tokens and no more row-groups than CUs
+    # (cfg0, the small golden cases) normally run on the K-parallel kernel;
+    # this keeps the row-wave kernel covered there
+    monkeypatch.setenv("KXW4_DECODE_KERNEL", "rowwave")
+
+
+def test_baseline_cfg0_rowwave(rowwave):
+    run_config("cfg0")
+
+
+@pytest.mark.parametrize("name", ["cfg128", "cfg64"])
+def test_exact_golden_rowwave(golden, name, rowwave):
+    test_exact_golden(golden, name)
+
+
 @pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
 def test_baseline_config_kparallel(name, kparallel):
     run_config(name)
