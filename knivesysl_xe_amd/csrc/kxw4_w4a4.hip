@@ -404,17 +404,24 @@ static int launch_w4(W4a4Args &a, hipStream_t st) {
 }
 
 int launch_w4a4(W4a4Args &a, hipStream_t st) {
-    // Default 128 x 64 (three work-groups per CU). The 64 x 160 tile (10
-    // waves, one work-group per CU) balances the cfg2 M=512 grid better but
-    // measures slower (207 vs 192 us): with one token block per wave the
-    // zero-point weight unpack is no longer shared. KXW4_W4A4_TILE=0..3 picks
-    // one configuration (tests, tuning).
+    // Default 128 x 64 (three work-groups per CU); when that grid gives fewer
+    // than two work-groups per CU, 64 x 64 (twice the work-groups, more waves
+    // per SIMD to overlap one wave's chain with another's MFMAs: cfg2 M=512
+    // 196 -> 184 us). The 64 x 160 tile (10 waves, one work-group per CU)
+    // balances the cfg2 M=512 grid but measures slower (207 us): with one
+    // token block per wave the zero-point weight unpack is no longer shared.
+    // KXW4_W4A4_TILE=0..4 picks one configuration (tests, tuning).
     const char *cfg = getenv("KXW4_W4A4_TILE");
-    const int sel = cfg ? atoi(cfg) : 0;
+    int sel = cfg ? atoi(cfg) : -1;
+    if (sel < 0) {
+        const long long tiles = (long long)((a.T + 127) / 128) * ((a.M / 16 + 3) / 4);
+        sel = tiles < 2LL * device_cus() ? 4 : 0;
+    }
     switch (sel) {
     case 3: return launch_w4<1, 1, 2, 5, 3, 3>(a, st);      // 64 tokens x 160 rows, 10 waves
     case 1: return launch_w4<2, 1, 2, 4, 3, 2>(a, st);      // 128 tokens x 128 rows, 8 waves
     case 2: return launch_w4<1, 2, 2, 2, 3, 2>(a, st);      // 64 tokens x 128 rows, 4 waves
+    case 4: return launch_w4<1, 1, 2, 2, 3, 3>(a, st);      // 64 tokens x 64 rows, 4 waves
     default: return launch_w4<2, 1, 2, 2, 3, 2>(a, st);     // 128 tokens x 64 rows, 4 waves
     }
 }

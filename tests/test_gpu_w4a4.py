@@ -88,7 +88,7 @@ def oracle_w4a4(codes, scales, x, residual=None, out_bf16=False, rows=None):
                      residual=residual, out_bf16=out_bf16, rows=rows)
 
 
-@pytest.fixture(params=["0", "1", "2", "3"])
+@pytest.fixture(params=["0", "1", "2", "3", "4"])
 def w4a4_tile(request, monkeypatch):
     monkeypatch.setenv("KXW4_W4A4_TILE", request.param)
     return request.param
