@@ -353,12 +353,15 @@ def machine_probes(head_bytes):
         ops.probe_read(buf, sink, shape)
         secs = timed(lambda _i: ops.probe_read(buf, sink, shape), 5)
         best_full = max(best_full, (buf.numel() / secs / 1e9, shape))
-        secs = timed(lambda i: ops.probe_read(slices[i % len(slices)], sink, shape), 2 * len(slices))
-        best_head = max(best_head, (n / secs / 1e9, shape))
+        # the headline's byte count, timed like the headline: launches over
+        # rotated slices captured in one graph and replayed between syncs
+        secs, _ = time_graph(lambda sl: ops.probe_read(sl, sink, shape), slices, 2 * len(slices), 2)
+        best_head = max(best_head, (n * 2 * len(slices) / secs / 1e9, shape))
     out["hbm_read_2GiB_GBps"], out["hbm_read_2GiB_shape"] = best_full
     out["hbm_read_headline_bytes_GBps"], out["hbm_read_headline_bytes_shape"] = best_head
     out["read_sample"] = (f"fastest of {ops.probe_read_shapes()} launch shapes; 2 GiB: 5 sweeps; headline "
-                          f"bytes: {len(slices)} slices of {n} bytes rotated through 2 GiB, back-to-back launches")
+                          f"bytes: {len(slices)} slices of {n} bytes rotated through 2 GiB, graph replay of "
+                          f"{2 * len(slices)} launches as for the headline")
     del buf
     return out
 
