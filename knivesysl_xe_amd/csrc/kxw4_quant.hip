@@ -141,17 +141,17 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
 // 64h + 16(c & 3) + 8((c >> 2) & 1), one 8-byte store. The four chunks of a
 // K32 block sit in four consecutive lanes, so their code sum is a 4-lane
 // shuffle.
-template <int P, int NCH>
-__global__ __launch_bounds__(kQThreads) void quantize_tok_kernel(QuantArgs a) {
+template <int P, int NCH, int NT = kQThreads>
+__global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
     static_assert(P == kLoadF32 || P == kLoadBF16, "plain loads");
-    __shared__ float red[kQThreads / 64];
+    __shared__ float red[NT / 64];
     const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
     const int nch = K / 8;
     float v[NCH][8];
     float mx = -INFINITY;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int idx = tid + c * kQThreads;
+        const int idx = tid + c * NT;
         if (idx < nch) {
             if constexpr (P == kLoadBF16) {
                 const uint4 x = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + (size_t)t * K)[idx];
@@ -171,13 +171,20 @@ __global__ __launch_bounds__(kQThreads) void quantize_tok_kernel(QuantArgs a) {
             for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
         }
     }
-    mx = block_reduce_max(mx, red);
+    // work-group max (order-free, so any thread count gives the same bits)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) mx = fmaxf(mx, red[i]);
     const float s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
     if (tid == 0) a.scale[t] = s;
     int8_t *qrow = a.q + (size_t)t * K;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int idx = tid + c * kQThreads;
+        const int idx = tid + c * NT;
         // whole K32 blocks (4 chunks) per 4-lane group: nch % 4 == 0
         if (idx - (tid & 3) < nch) {
             uint32_t lo = 0, hi = 0;
@@ -206,6 +213,16 @@ static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
         // one pass with the row in registers, up to 20480 elements
         const int nch = a.K / 8;
         if (block != 32 && a.K % 32 == 0) {
+            // few tokens: a row's work-group is most of the launch, so it
+            // takes 1024 threads (three times the loads in flight per row;
+            // T=1, K=17408: 6.3 -> ~3 us)
+            if (a.T < 64 && nch <= 3 * 1024) {
+                if (nch <= 1024)
+                    hipLaunchKernelGGL((quantize_tok_kernel<P, 1, 1024>), dim3(a.T), dim3(1024), 0, st, a);
+                else
+                    hipLaunchKernelGGL((quantize_tok_kernel<P, 3, 1024>), dim3(a.T), dim3(1024), 0, st, a);
+                return hipGetLastError() == hipSuccess ? 0 : -6;
+            }
             if (nch <= 2 * kQThreads)
                 hipLaunchKernelGGL((quantize_tok_kernel<P, 2>), dim3(a.T), dim3(kQThreads), 0, st, a);
             else if (nch <= 4 * kQThreads)
