@@ -409,7 +409,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the projection shards column- or row-parallel, see DESIGN.md)", file=sys.stderr)
+              "(the projection would shard column-parallel over row-groups, or row-parallel "
+              "over K with one all-reduce of the FP32 partials)", file=sys.stderr)
         sys.exit(2)
 
     import torch
