@@ -49,15 +49,17 @@
  *                    (row, col) owns a distinct contiguous 6-bit field of its
  *                    384-byte tile; the bit positions themselves restate
  *                    kernels_core.cpp:46-75 and no reference vector checks them
- *   orc_fit_int8     known answers (exactly representable groups reproduce
- *                    their step, clamp asymmetry at -128/127) and invariants;
- *                    the refinement's rounding on general inputs restates
- *                    kernels_dpas.cpp:363-377 (parity unpinned beyond those)
- *   orc_fit_int4_asym parity unpinned beyond known answers and invariants
- *                    (exact fits of evenly spaced groups, zero kept, nibble
- *                    reserved, codes within half a step); the least-squares
- *                    refinement's rounding on general inputs restates
- *                    kernels_dpas.cpp:229-256 unchecked
+ *   orc_fit_int8     hand-derived known answers (tests/test_oracle.py):
+ *                    a group whose scale moves in both refinements (one or
+ *                    three refinements, or the negative side over 127, give
+ *                    other bits), grid-exact groups, the -128/127 clamp
+ *                    asymmetry, all-zero => 1.0; plus invariants
+ *   orc_fit_int4_asym hand-derived known answers: the (sh + 8) & 0xFFF0
+ *                    nibble round-up (nibbles 7, 8, 9: truncation and
+ *                    round-to-even fail), a group whose scale moves in all
+ *                    three refinements (two or four fail), all-positive and
+ *                    all-negative groups whose range must start at 0 (a
+ *                    range seeded from the data fails); plus invariants
  *   contract         selects how a chain step `acc += x*y` (and the fit's
  *                    least-squares sums) round: 1 = one fused multiply-add,
  *                    what icpx's default contraction makes of the

@@ -166,6 +166,80 @@ def test_fit_int4_asym_known_answer():
     assert (sh, z) == (0x3C00, -8)
 
 
+@pytest.mark.parametrize("contract", [True, False])
+def test_fit_int4_asym_nibble_reserve_rounds_up(contract):
+    # fit_int4_asym stores (sh + 8) & 0xFFF0 (kernels_dpas.cpp:254-255): the
+    # scale's low nibble is rounded half up into the next 16-ulp step, not
+    # truncated and not rounded to even. Groups on an exact grid
+    # w_j = s*(j-8), j = 0..15, keep s through the fit: lo = -8s, hi = 7s,
+    # (hi-lo)/15 = s exactly; zi = rint(8s/s) - 8 = 0; codes q_j = j-8, so
+    # num = 344*s and den = 344 (sum of c^2 over c = -8..7) are exact and
+    # num/den = s in every refinement; z = 0.
+    def grid(step):
+        return (np.float32(step) * (np.arange(16) - 8)).astype(np.float32)
+    # s = 1033/1024: fp16 0x3C09, nibble 9 -> 0x3C11 & 0xFFF0 = 0x3C10
+    # (truncation would give 0x3C00)
+    assert O.fit_int4_asym(grid(1033 / 1024), contract=contract) == (0x3C10, 0)
+    # s = 129/128: fp16 0x3C08, nibble 8 (a tie) -> 0x3C10 (rounding the
+    # nibble to even would keep 0x3C00)
+    assert O.fit_int4_asym(grid(129 / 128), contract=contract) == (0x3C10, 0)
+    # s = 1031/1024: fp16 0x3C07, nibble 7 -> 0x3C0F & 0xFFF0 = 0x3C00
+    assert O.fit_int4_asym(grid(1031 / 1024), contract=contract) == (0x3C00, 0)
+    # without the reservation the FP16 bits are returned as they are
+    assert O.fit_int4_asym(grid(1033 / 1024), reserve_nibble=False, contract=contract) == (0x3C09, 0)
+
+
+@pytest.mark.parametrize("contract", [True, False])
+def test_fit_int4_asym_three_refinements(contract):
+    # A group whose scale moves in each of the three least-squares
+    # refinements (kernels_dpas.cpp:239-251). Integer weights keep every num
+    # and den an exact integer (so the FMA contraction cannot matter); only
+    # the divisions round, and no rint below is within 0.05 of a tie.
+    #   w = [5,0,0,-4,7,7,7,0,0,0,-4,0,0,0,0,0]: lo = -4, hi = 7
+    #   s0 = 11/15 = 0.73333335
+    #   refinement 1: zi = rint(4/s0) - 8 = rint(5.4545) - 8 = -3
+    #     w/s0 + zi: 5 -> 3.818 -> q 4, c 7; -4 -> -8.455 -> q -8, c -5;
+    #     7 -> 6.545 -> q 7, c 10; 0 -> q -3, c 0
+    #     num = 5*7 + 2*(-4)(-5) + 3*7*10 = 285, den = 49 + 2*25 + 3*100 = 399
+    #     s1 = 285/399 = 0.71428573
+    #   refinement 2: zi = rint(4/s1) - 8 = rint(5.6) - 8 = -2
+    #     5 -> 7.0 - 2 = 5 -> c 7; -4 -> -7.6 -> q -8, c -6; 7 -> 7.8 -> q 7, c 9
+    #     num = 35 + 2*24 + 3*63 = 272, den = 49 + 2*36 + 3*81 = 364
+    #     s2 = 272/364 = 0.74725276
+    #   refinement 3: zi = rint(4/s2) - 8 = rint(5.353) - 8 = -3
+    #     5 -> 3.691 -> q 4, c 7; -4 -> -8.353 -> q -8, c -5; 7 -> 6.368 -> q 6, c 9
+    #     num = 35 + 40 + 189 = 264, den = 49 + 50 + 243 = 342
+    #     s3 = 264/342 = 0.7719298
+    #   z = rint(4/s3) - 8 = rint(5.182) - 8 = -3
+    #   fp16(s3) = 0x3A2D (1.5439 * 2^-1, mantissa rint(556.9) = 557)
+    #   -> (0x3A2D + 8) & 0xFFF0 = 0x3A30
+    # Two refinements would store fp16(s2) = 0x39FA -> 0x3A00; four would
+    # give 0x3A50.
+    w = np.array([5, 0, 0, -4, 7, 7, 7, 0, 0, 0, -4, 0, 0, 0, 0, 0], np.float32)
+    assert O.fit_int4_asym(w, contract=contract) == (0x3A30, -3)
+    assert O.fit_int4_asym(w, reserve_nibble=False, contract=contract) == (0x3A2D, -3)
+    # the same group inside K32 and K64 groups (zeros do not change num, den,
+    # lo or hi)
+    for n in (32, 64):
+        wn = np.zeros(n, np.float32)
+        wn[:16] = w
+        assert O.fit_int4_asym(wn, contract=contract) == (0x3A30, -3)
+
+
+def test_fit_int4_asym_range_includes_zero():
+    # lo and hi start at 0, so the fitted range always includes 0
+    # (kernels_dpas.cpp:231-236); a range seeded from the data would differ.
+    # All +2: lo = 0, hi = 2, s0 = 2/15 = 0.13333334; zi = rint(0/s0) - 8 = -8;
+    # every w/s0 - 8 = 7 -> q 7, c 15; num = 16*2*15 = 480, den = 16*225 =
+    # 3600, s = 480/3600 = 0.13333334 again (three times); z = -8;
+    # fp16(s) = 0x3044 -> 0x3040. (A range seeded from the data, lo = hi = 2,
+    # gives s = 0 -> 1 and stays there: 0x3C00.)
+    assert O.fit_int4_asym(np.full(16, 2.0, np.float32)) == (0x3040, -8)
+    # All -2: lo = -2, hi = 0, s0 = 2/15; zi = rint(2/s0) - 8 = rint(15) - 8 =
+    # 7; w/s0 + 7 = -8 -> q -8, c -15; num = 480, den = 3600; z = 7 -> 0x3040.
+    assert O.fit_int4_asym(np.full(16, -2.0, np.float32)) == (0x3040, 7)
+
+
 def test_fit_int4_asym_reserves_nibble_and_keeps_zero():
     rng = np.random.default_rng(6)
     for _ in range(200):
@@ -503,6 +577,30 @@ def test_fit_int8_known_answers():
     wf[7] = -1.0
     assert O.fit_int8(wf) == 0x2000                              # fp16(1/128)
     assert O.fit_int8(np.zeros(32, np.float32)) == 0x3C00        # scale 1
+
+
+@pytest.mark.parametrize("contract", [True, False])
+def test_fit_int8_two_refinements_and_negative_side(contract):
+    # w8_repack_kernel's fit (kernels_dpas.cpp:358-380) on a K32 group of
+    # integers (num and den exact; only the divisions round, no rint within
+    # 0.01 of a tie):
+    #   w: -16 at 6 and 7, 23 at 10, 26 and 30, -39 at 29, 0 elsewhere
+    #   hi = 23, neg = 39: s0 = max(23/127, 39/128) = 39/128 = 0.3046875
+    #   refinement 1: -16/s0 = -52.513 -> -53; 23/s0 = 75.487 -> 75; -39 -> -128
+    #     num = 2*16*53 + 3*23*75 + 39*128 = 11863
+    #     den = 2*53^2 + 3*75^2 + 128^2 = 38877; s1 = 0.30514187
+    #   refinement 2: -16/s1 = -52.435 -> -52; 23/s1 = 75.375 -> 75;
+    #     -39/s1 = -127.81 -> -128
+    #     num = 2*16*52 + 5175 + 4992 = 11831, den = 5408 + 16875 + 16384 = 38667
+    #     s2 = 11831/38667 = 0.3059715
+    #   fp16(s2) = 1.22389 * 2^-2: mantissa rint(229.26) = 229 -> 0x34E5
+    # One refinement would store fp16(s1) = 0x34E2, three 0x34E9; the
+    # negative side divided by 127 instead of 128 also ends at 0x34E9.
+    w = np.zeros(32, np.float32)
+    w[[6, 7]] = -16
+    w[[10, 26, 30]] = 23
+    w[29] = -39
+    assert O.fit_int8(w, contract=contract) == 0x34E5
 
 
 def test_fit_int8_invariants():
