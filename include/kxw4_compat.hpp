@@ -15,7 +15,10 @@
 //     the reference's [K/64][T] layout;
 //   * every call runs on the stream set by kxw4_compat_set_stream (the null
 //     stream by default), the counterpart of the reference's one in-order
-//     queue per rank (decode.cpp:86-99).
+//     queue per rank (decode.cpp:86-99);
+//   * x_gemv_w4a8_prepared / x_gemv_w8a8_prepared return -2 unless the last
+//     prepare had the weight's K; the reference checks only the scratch
+//     capacity (kernels_dpas.cpp:1636) and would read a stale activation.
 // Like the reference, the prepared activation (x_prepare_gemv_act_s8,
 // x_silu_mul_quant, x_rmsnorm_quant) lives in library-owned grow-only scratch
 // and stays valid until the next prepare; these calls are not thread-safe.

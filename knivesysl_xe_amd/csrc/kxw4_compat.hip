@@ -178,6 +178,10 @@ void x_rmsnorm_chunk(float *d_out, const float *d_in, const uint16_t *d_w, int H
 int x_gemv_w4a8_prepared(const tq_qmma_weight_t *w, float *d_y, const float *d_residual) {
     // every W4 tier, K16 included (kernels_dpas.cpp:1647-1653)
     if (!w || !w->s4_ready || !w->d_s4 || !w->d_s4_scale || !d_y) return -1;
+    // -2 when no activation of this K is prepared. The reference checks only
+    // the scratch capacity (kernels_dpas.cpp:1636), so after a prepare of a
+    // different K within that capacity it returns 0 and reads the stale
+    // codes; this shim refuses that case with the same -2.
     if (g_act.K != w->K) return -2;
     const kxw4_weight_t d = w4_of(w);
     const kxw4_act_t a = prepared_act();
@@ -218,9 +222,23 @@ void x_quantize_act_chunk(const float *d_x, int K, int T, int8_t *d_aq, float *d
     kxw4_quantize_act(d_x, KXW4_F32, T, K, 32, d_aq, d_as, d_asum, g_stream);
 }
 
+// x_gemm_w4a8's checks (kernels_dpas.cpp:1337-1367): -1 for a weight that
+// is not a K32/K64 W4 tier, -2 for missing operands, T not a positive
+// multiple of 8, and offsets that do not partition [0, T) in multiples of 8
+// (at most 8 segments). Ragged segments stay on the C ABI (kxw4_gemm).
 int x_gemm_w4a8(const tq_qmma_weight_t *w, const int8_t *d_aq, const float *d_as,
                 const int32_t *d_asum, float *d_y, int T, const int *offsets, int segments) {
-    if (!w4_ready(w) || !d_aq || !d_as || !d_asum || !d_y) return -1;
+    if (!w4_ready(w)) return -1;
+    if (!d_aq || !d_as || !d_asum || !d_y || T <= 0 || (T % 8) != 0) return -2;
+    if (offsets) {
+        if (segments < 1 || segments > 8 || offsets[0] != 0 || offsets[segments] != T) return -2;
+        for (int i = 0; i < segments; ++i)
+            if (offsets[i] < 0 || offsets[i + 1] <= offsets[i] || offsets[i + 1] > T || offsets[i] % 8 ||
+                offsets[i + 1] % 8)
+                return -2;
+    } else if (segments != 0) {
+        return -2;
+    }
     const kxw4_weight_t d = w4_of(w);
     kxw4_act_t a;
     a.T = T;

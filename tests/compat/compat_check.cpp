@@ -374,6 +374,22 @@ int main() {
     check(x_gemv_w4a8_fanout(ws, ys, 5) == -1, "fan-out count 5 = -1");
     const int bad_off[3] = {0, 80, T};
     check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, bad_off, 2) == -2, "GEMM offsets past T = -2");
+    // x_gemm_w4a8's -2 cases (kernels_dpas.cpp:1338, 1349-1356, 1364)
+    check(x_gemm_w4a8(&w32, nullptr, das, dasum, dyt, T, nullptr, 0) == -2, "x_gemm_w4a8 null aq = -2");
+    check(x_gemm_w4a8(&w32, daq, nullptr, dasum, dyt, T, nullptr, 0) == -2, "x_gemm_w4a8 null as = -2");
+    check(x_gemm_w4a8(&w32, daq, das, nullptr, dyt, T, nullptr, 0) == -2, "x_gemm_w4a8 null asum = -2");
+    check(x_gemm_w4a8(&w32, daq, das, dasum, nullptr, T, nullptr, 0) == -2, "x_gemm_w4a8 null y = -2");
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, 0, nullptr, 0) == -2, "x_gemm_w4a8 T = 0 = -2");
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, 36, nullptr, 0) == -2, "x_gemm_w4a8 T % 8 != 0 = -2");
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, nullptr, 1) == -2, "x_gemm_w4a8 segments without offsets = -2");
+    const int off_ragged[3] = {0, 12, T};
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, off_ragged, 2) == -2, "x_gemm_w4a8 offset % 8 != 0 = -2");
+    const int off_first[3] = {8, 16, T};
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, off_first, 2) == -2, "x_gemm_w4a8 offsets[0] != 0 = -2");
+    const int off_empty[3] = {0, 0, T};
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, off_empty, 2) == -2, "x_gemm_w4a8 empty segment = -2");
+    check(x_gemm_w4a8(&w32, daq, das, dasum, dyt, T, offsets, 9) == -2, "x_gemm_w4a8 9 segments = -2");
+    check(x_gemm_w4a8(nullptr, daq, das, dasum, dyt, T, nullptr, 0) == -1, "x_gemm_w4a8 null weight = -1");
 
     std::printf("compat: %d passed, %d failed\n", g_pass, g_fail);
     return g_fail ? 1 : 0;
