@@ -51,6 +51,28 @@ def _ptr(t: Optional[torch.Tensor]):
     return C.c_void_p(t.data_ptr())
 
 
+def _need(t, name: str, dtypes, shape, device) -> torch.Tensor:
+    """Validate a caller-supplied buffer before its pointer reaches a kernel:
+    a tensor on `device` (the weight's GPU), contiguous, of one of `dtypes` and exactly
+    `shape`. The kernels trust these sizes, so a mismatch raises here."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.device != torch.device(device):
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if isinstance(dtypes, torch.dtype):
+        dtypes = (dtypes,)
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} must be {' or '.join(str(d) for d in dtypes)}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+_BITS16 = (torch.int16, torch.uint16) if hasattr(torch, "uint16") else (torch.int16,)
+
+
 def _dtype_code(dt: torch.dtype) -> int:
     if dt == torch.float32:
         return F32
@@ -241,7 +263,10 @@ def s4_codes_natural(a: QuantActS4) -> torch.Tensor:
 
 
 def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor, block: int = 32, keep_hidden=True):
+    """SiLU(gate) * up of [T][K] f32 rows, quantized (x_silu_mul_quant)."""
     T, K = gate.shape
+    _need(gate, "gate", torch.float32, (T, K), gate.device)
+    _need(up, "up", torch.float32, (T, K), gate.device)
     a = QuantAct.empty(T, K, block, gate.device)
     hidden = torch.empty(T, K, dtype=torch.float32, device=gate.device) if keep_hidden else None
     check("kxw4_silu_mul_quant", lib().kxw4_silu_mul_quant(
@@ -252,7 +277,11 @@ def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor, block: int = 32, keep_h
 
 def rmsnorm_quant(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, block: int = 32,
                   keep_normed=True):
+    """(1+w) RMSNorm of [T][H] f32 rows fused with the quantizer
+    (x_rmsnorm_quant); w is [H] BF16 bits (int16 or bfloat16)."""
     T, H = x.shape
+    _need(x, "x", torch.float32, (T, H), x.device)
+    _need(w_bf16_bits, "w", _BITS16 + (torch.bfloat16,), (H,), x.device)
     a = QuantAct.empty(T, H, block, x.device)
     out = torch.empty(T, H, dtype=torch.float32, device=x.device) if keep_normed else None
     check("kxw4_rmsnorm_quant", lib().kxw4_rmsnorm_quant(
@@ -264,21 +293,52 @@ def rmsnorm_quant(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, block:
 def rmsnorm(x: torch.Tensor, w_bf16_bits: torch.Tensor, eps: float, out=None) -> torch.Tensor:
     """Batched (1+w) RMSNorm of [T][H] f32 rows (x_rmsnorm_chunk)."""
     T, H = x.shape
+    _need(x, "x", torch.float32, (T, H), x.device)
+    _need(w_bf16_bits, "w", _BITS16 + (torch.bfloat16,), (H,), x.device)
+    if out is not None:
+        _need(out, "out", torch.float32, (T, H), x.device)
     y = out if out is not None else torch.empty(T, H, dtype=torch.float32, device=x.device)
     check("kxw4_rmsnorm", lib().kxw4_rmsnorm(_ptr(y), _ptr(x), _ptr(w_bf16_bits), T, H, eps,
                                              _stream()))
     return y
 
 
-def _out(T: int, M: int, dtype, device, out=None):
+def _out(T: int, M: int, dtype, device, out=None, name="out"):
+    """The [T][M] output buffer: `out` after validation, else a new tensor."""
+    _dtype_code(dtype)
     if out is not None:
-        return out
+        return _need(out, name, dtype, (T, M), device)
     return torch.empty(T, M, dtype=dtype, device=device)
+
+
+def _residual(residual, T: int, M: int, device):
+    if residual is not None:
+        _need(residual, "residual", torch.float32, (T, M), device)
+    return residual
+
+
+def _check_weight(w: "W4Weight", device):
+    if not torch.device(device).type == "cuda":
+        raise ValueError("weights must be on the GPU")
+    nbytes = w.M * w.K if w.scale_enc == SCALE_W8 else w.M * w.K // 2
+    _need(w.codes, "weight codes", torch.uint8, (nbytes,), device)
+    _need(w.scales, "weight scales", _BITS16, (w.M * (w.K // w.group),), device)
+
+
+def _check_act(a: QuantAct, device):
+    _need(a.q, "activation codes", torch.int8, (a.T, a.K), device)
+    _need(a.scale, "activation scales", torch.float32,
+          (a.T, a.K // 32) if a.block == 32 else (a.T,), device)
+    _need(a.sum, "activation sums", torch.int32, (a.T, a.K // 32), device)
 
 
 def gemv(w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None, splits: int = 0,
          out=None) -> torch.Tensor:
-    y = _out(a.T, w.M, dtype, a.q.device, out)
+    dev = w.codes.device
+    _check_weight(w, dev)
+    _check_act(a, dev)
+    y = _out(a.T, w.M, dtype, dev, out)
+    _residual(residual, a.T, w.M, dev)
     wc, ac = w.c(), a.c()
     check("kxw4_gemv", lib().kxw4_gemv(C.byref(wc), C.byref(ac), _ptr(y), _dtype_code(dtype),
                                        _ptr(residual), splits, _stream()))
@@ -291,8 +351,19 @@ def _weight_array(ws: Sequence[W4Weight]):
     return cs, arr
 
 
+def _outs(ws: Sequence[W4Weight], T: int, dtype, device, outs):
+    if outs is not None and len(outs) != len(ws):
+        raise ValueError(f"outs has {len(outs)} tensors for {len(ws)} weights")
+    return [_out(T, w.M, dtype, device, None if outs is None else outs[i], f"outs[{i}]")
+            for i, w in enumerate(ws)]
+
+
 def gemv_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, outs=None):
-    ys = outs if outs is not None else [_out(a.T, w.M, dtype, a.q.device) for w in ws]
+    dev = ws[0].codes.device
+    for w in ws:
+        _check_weight(w, dev)
+    _check_act(a, dev)
+    ys = _outs(ws, a.T, dtype, dev, outs)
     keep, warr = _weight_array(ws)
     yarr = (C.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
     ac = a.c()
@@ -310,7 +381,11 @@ def _offsets(offsets):
 
 def gemm(w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None, offsets=None,
          forced_splits: int = 0, out=None) -> torch.Tensor:
-    y = _out(a.T, w.M, dtype, a.q.device, out)
+    dev = w.codes.device
+    _check_weight(w, dev)
+    _check_act(a, dev)
+    y = _out(a.T, w.M, dtype, dev, out)
+    _residual(residual, a.T, w.M, dev)
     off, nseg = _offsets(offsets)
     wc, ac = w.c(), a.c()
     check("kxw4_gemm", lib().kxw4_gemm(C.byref(wc), C.byref(ac), _ptr(y), _dtype_code(dtype),
@@ -320,7 +395,11 @@ def gemm(w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None, offsets=N
 
 def gemm_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offsets=None,
                 forced_splits: int = 0, outs=None):
-    ys = outs if outs is not None else [_out(a.T, w.M, dtype, a.q.device) for w in ws]
+    dev = ws[0].codes.device
+    for w in ws:
+        _check_weight(w, dev)
+    _check_act(a, dev)
+    ys = _outs(ws, a.T, dtype, dev, outs)
     keep, warr = _weight_array(ws)
     yarr = (C.c_void_p * len(ws))(*[y.data_ptr() for y in ys])
     off, nseg = _offsets(offsets)
@@ -334,7 +413,15 @@ def gemm_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offset
 def gemm_w4a4(w: W4Weight, a: QuantActS4, dtype=torch.float32, residual=None,
               out=None) -> torch.Tensor:
     """W4A4 GEMM of s4 activations against a K64 weight with FP16|zp scales."""
-    y = _out(a.T, w.M, dtype, a.q4.device, out)
+    dev = w.codes.device
+    _check_weight(w, dev)
+    _need(a.q4, "s4 codes", torch.uint8, (a.K // 128, a.T, 64), dev)
+    _need(a.scale, "s4 scales", torch.float32, (a.K // 64, a.T), dev)
+    _need(a.sum, "s4 sums", torch.int32, (a.K // 64, a.T), dev)
+    if a.K != w.K:
+        raise ValueError(f"activation K {a.K} != weight K {w.K}")
+    y = _out(a.T, w.M, dtype, dev, out)
+    _residual(residual, a.T, w.M, dev)
     wc = w.c()
     check("kxw4_gemm_w4a4", lib().kxw4_gemm_w4a4(
         C.byref(wc), _ptr(a.q4), _ptr(a.scale), _ptr(a.sum), a.T, _ptr(y), _dtype_code(dtype),
@@ -409,6 +496,24 @@ def partials(w: W4Weight, a: QuantAct) -> torch.Tensor:
     wc, ac = w.c(), a.c()
     check("kxw4_partials", lib().kxw4_partials(C.byref(wc), C.byref(ac), _ptr(P), _stream()))
     return P
+
+
+class option:
+    """Set one kernel-selection option (kxw4_set_option) for a `with` block
+    and restore its previous value afterwards, e.g.
+    `with ops.option("decode_kernel", 1): ...` for the K-parallel kernel."""
+
+    def __init__(self, name: str, value: int):
+        self.name, self.value, self.prev = name, int(value), None
+
+    def __enter__(self):
+        prev = C.c_int()
+        check("kxw4_set_option", lib().kxw4_set_option(self.name.encode(), self.value, C.byref(prev)))
+        self.prev = prev.value
+        return self
+
+    def __exit__(self, *exc):
+        check("kxw4_set_option", lib().kxw4_set_option(self.name.encode(), self.prev, None))
 
 
 def gemv_splits(groups: int) -> int:
