@@ -91,6 +91,24 @@ typedef struct kxw4_act {
 int kxw4_abi_version(void);
 const char *kxw4_error_string(int code);
 
+/* Kernel-selection options, process-wide, for A/B timing and tests (the
+ * counterpart of the reference's once-per-process TQ_XPU_GEMM_SPLITS read,
+ * kernels_dpas.cpp:1227-1233; the split override itself is the explicit
+ * `forced_splits` argument of kxw4_gemm). Each option starts from the
+ * environment variable KXW4_<NAME> read once per process; the defaults pick
+ * the kernels measured fastest and the results are the same bits either way.
+ *   decode_kernel      0 auto, 1 K-parallel kernel only, 2 row-wave kernel
+ *                      wherever it applies
+ *   rowwave_rpw        row-groups per row-wave work-group, 0 = launcher's plan
+ *   rowwave_plain_grid 1 = plain work-groups even with a partial last round
+ *   gemm_kernel        0 auto, 1 the general GEMM for every prefill shape
+ *   gemm3_tile         -1 cost model, 0..9 one 32x32x32 GEMM tile
+ *   w4a4_tile          -1 default rule, 0..4 one W4A4 GEMM tile
+ * Returns 0, -1 for an unknown name, -2 for a value out of range; *previous
+ * (may be NULL) receives the old value. Not synchronised with launches in
+ * flight on other host threads. */
+int kxw4_set_option(const char *name, int value, int *previous);
+
 /* Bytes of packed codes and number of scale entries of one weight. */
 size_t kxw4_code_bytes(int M, int K);
 size_t kxw4_scale_count(int M, int K, int group);

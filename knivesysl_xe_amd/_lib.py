@@ -40,6 +40,7 @@ AP = C.POINTER(Act)
 SIGNATURES = {
     "kxw4_abi_version": (I, []),
     "kxw4_error_string": (C.c_char_p, [I]),
+    "kxw4_set_option": (I, [C.c_char_p, I, C.POINTER(I)]),
     "kxw4_code_bytes": (C.c_size_t, [I, I]),
     "kxw4_scale_count": (C.c_size_t, [I, I, I]),
     "kxw4_gemv_splits": (I, [I]),

@@ -5,8 +5,62 @@
 #include "kxw4_internal.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 using namespace kxw4;
+
+namespace kxw4 {
+
+namespace {
+
+struct OptionDesc {
+    const char *name;
+    int Options::*field;
+    int lo, hi;
+};
+
+const OptionDesc kOptions[] = {
+    {"decode_kernel", &Options::decode_kernel, kDecodeAuto, kDecodeRowwave},
+    {"rowwave_rpw", &Options::rowwave_rpw, 0, 16},
+    {"rowwave_plain_grid", &Options::rowwave_plain_grid, 0, 1},
+    {"gemm_kernel", &Options::gemm_kernel, kGemmAuto, kGemmGeneral},
+    {"gemm3_tile", &Options::gemm3_tile, -1, 9},
+    {"w4a4_tile", &Options::w4a4_tile, -1, 4},
+};
+
+// The environment is read once, when the library first selects a kernel.
+Options from_env() {
+    Options o;
+    if (const char *e = getenv("KXW4_DECODE_KERNEL")) {
+        if (!strcmp(e, "kparallel")) o.decode_kernel = kDecodeKParallel;
+        else if (!strcmp(e, "rowwave")) o.decode_kernel = kDecodeRowwave;
+    }
+    auto num = [](const char *name, int lo, int hi, int &dst) {
+        const char *e = getenv(name);
+        if (!e || !*e) return;
+        const int v = atoi(e);
+        if (v >= lo && v <= hi) dst = v;
+    };
+    num("KXW4_ROWWAVE_RPW", 0, 16, o.rowwave_rpw);
+    num("KXW4_ROWWAVE_PLAIN_GRID", 0, 1, o.rowwave_plain_grid);
+    if (const char *e = getenv("KXW4_GEMM_KERNEL"))
+        if (!strcmp(e, "general")) o.gemm_kernel = kGemmGeneral;
+    num("KXW4_GEMM3_TILE", -1, 9, o.gemm3_tile);
+    num("KXW4_W4A4_TILE", -1, 4, o.w4a4_tile);
+    return o;
+}
+
+Options &mutable_options() {
+    static Options o = from_env();
+    return o;
+}
+
+}  // namespace
+
+const Options &options() { return mutable_options(); }
+
+}  // namespace kxw4
 
 namespace {
 
@@ -159,6 +213,19 @@ int decode_uniform(const kxw4_weight_t *const *ws, void *const *ys, int count,
 extern "C" {
 
 int kxw4_abi_version(void) { return KXW4_ABI_VERSION; }
+
+int kxw4_set_option(const char *name, int value, int *previous) {
+    if (!name) return KXW4_EARG;
+    for (const OptionDesc &d : kOptions) {
+        if (strcmp(d.name, name) != 0) continue;
+        if (value < d.lo || value > d.hi) return KXW4_ESHAPE;
+        Options &o = mutable_options();
+        if (previous) *previous = o.*(d.field);
+        o.*(d.field) = value;
+        return KXW4_OK;
+    }
+    return KXW4_EARG;
+}
 
 const char *kxw4_error_string(int code) {
     switch (code) {

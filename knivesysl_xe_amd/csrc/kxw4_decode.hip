@@ -29,8 +29,6 @@
 #include "kxw4_internal.hpp"
 
 #include <algorithm>
-#include <cstdlib>
-#include <cstring>
 
 namespace kxw4 {
 
@@ -328,30 +326,23 @@ int device_cus() {
 }
 
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
-    // Up to 16 tokens go to the row-wave kernel, the rest stay here.
-    // KXW4_DECODE_KERNEL=persist tries the persistent kernel first (up to 8
-    // tokens with one split plan per weight); =kparallel skips the row-wave
-    // kernel and =rowwave prefers it (used by the tests to cover every kernel
-    // at the decode shapes).
+    // Up to 16 tokens go to the row-wave kernel, the rest stay here. The
+    // decode_kernel option forces the K-parallel kernel (kparallel) or
+    // prefers the row-wave kernel (rowwave); the tests use both to cover
+    // every kernel at the decode shapes.
     // W8 and K16 weights run on the row-wave kernel only; 1 hands the shape
     // back to the caller (the GEMM path for W8)
     if (a.w8 || a.group == 16) return debug ? 1 : launch_rowwave(a, st);
-    const char *force = getenv("KXW4_DECODE_KERNEL");
-    const bool use_persist = force && strcmp(force, "persist") == 0;
-    bool no_rowwave = force && strcmp(force, "kparallel") == 0;
+    const int force = options().decode_kernel;
+    bool no_rowwave = force == kDecodeKParallel;
     // Per-token weights with at most 8 tokens and no more row-groups than
     // CUs stay here: one work-group per row-group whose waves read
     // consecutive kilobytes beats the row-wave kernel's per-split streams
     // when every CU holds at most one row-group (cfg0: 6.9 -> 6.3 us).
-    // KXW4_DECODE_KERNEL=rowwave keeps them on the row-wave kernel.
-    if (!(force && strcmp(force, "rowwave") == 0) && a.block == 0 && a.scale_enc == 0 && a.T <= 8) {
+    if (force != kDecodeRowwave && a.block == 0 && a.scale_enc == 0 && a.T <= 8) {
         int rgs = 0;
         for (int i = 0; i < a.count; ++i) rgs += a.w[i].M / 16;
         if (rgs <= device_cus()) no_rowwave = true;
-    }
-    if (!debug && use_persist) {
-        const int r = launch_persist(a, st);
-        if (r != 1) return r;
     }
     if (!debug && !no_rowwave) {
         const int r = launch_rowwave(a, st);

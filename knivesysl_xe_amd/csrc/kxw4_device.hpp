@@ -94,6 +94,19 @@ __device__ __forceinline__ v4i rotate8(v4i v) {
     return r;
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// this wave are outstanding and leaves expcnt and lgkmcnt alone. The gfx9
+// encoding splits vmcnt over bits [3:0] and [15:14] (six bits, n <= 63);
+// expcnt is bits [6:4] (7 = no wait), lgkmcnt bits [11:8] (15 = no wait).
+constexpr int waitcnt_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+static_assert(waitcnt_vmcnt(0) == 0x0F70 && waitcnt_vmcnt(15) == 0x0F7F &&
+              waitcnt_vmcnt(16) == 0x4F70 && waitcnt_vmcnt(63) == 0xCF7F, "vmcnt encoding");
+#define KXW4_WAIT_VMCNT(n)                                                     \
+    do {                                                                       \
+        static_assert((n) >= 0 && (n) <= 63, "vmcnt holds six bits");          \
+        __builtin_amdgcn_s_waitcnt(::kxw4::waitcnt_vmcnt(n));                  \
+    } while (0)
+
 // Barrier for LDS traffic only: waits for this wave's LDS accesses, not for
 // its outstanding global loads, so a prefetch ring stays in flight.
 __device__ __forceinline__ void lds_sync() {

@@ -28,8 +28,6 @@
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
-#include <cstdlib>
-#include <cstring>
 
 namespace kxw4 {
 
@@ -375,18 +373,10 @@ static void launch_w8(const GemmArgs &a, bool splits, bool debug, dim3 grid, hip
 }
 
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
-    // The per-token, one-split mode goes to the large-tile kernel;
-    // KXW4_GEMM_KERNEL=gemm2 takes the smaller-tile LDS-DMA kernel, =general
-    // keeps it here (the tests cover all three).
-    const char *force = getenv("KXW4_GEMM_KERNEL");
-    const bool general = force && strcmp(force, "general") == 0;
-    const bool g2 = force && strcmp(force, "gemm2") == 0;
-    if (!debug && !general && !g2 && !a.w8) {
+    // The per-token, one-split mode goes to the large-tile kernel; the
+    // gemm_kernel option keeps it here (the tests cover both).
+    if (!debug && options().gemm_kernel != kGemmGeneral && !a.w8) {
         const int r = launch_gemm3(a, st);
-        if (r != 1) return r;
-    }
-    if (!debug && !general && !a.w8) {
-        const int r = launch_gemm2(a, st);
         if (r != 1) return r;
     }
     bool splits = false;

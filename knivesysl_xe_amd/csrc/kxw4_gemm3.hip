@@ -222,9 +222,9 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     int st = 0;
     for (int kb = 0; kb < NT; ++kb) {
         const int later = min(NST - 2, NT - 1 - kb);
-        if (NST >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LD));
-        else if (NST >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LD);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        if (NST >= 4 && later >= 2) KXW4_WAIT_VMCNT(2 * LD);
+        else if (NST >= 3 && later >= 1) KXW4_WAIT_VMCNT(LD);
+        else KXW4_WAIT_VMCNT(0);
         lds_sync_after_dma();
         if (kb + NST - 1 < NT) issue(kb + NST - 1, st == 0 ? NST - 1 : st - 1);
         const uint8_t *sb = smem + st * STAGE;
@@ -426,9 +426,8 @@ int launch_gemm3(GemmArgs &a, hipStream_t st) {
     //     one work-group per CU: fits the grid when the 256-row tile leaves
     //     CUs idle;
     //   128 x 64, 4 waves of 2 blocks, three work-groups per CU.
-    // KXW4_GEMM3_TILE=0..9 picks one configuration (tests, tuning).
-    const char *cfg = getenv("KXW4_GEMM3_TILE");
-    int sel = cfg ? atoi(cfg) : -1;
+    // the gemm3_tile option (0..9) picks one configuration (tests, tuning)
+    int sel = options().gemm3_tile;
     if (sel < 0) {
         const bool g128 = a.group == 128;
         struct Cand { int sel, bm, bng, wgs, simd_blocks; double penalty; };

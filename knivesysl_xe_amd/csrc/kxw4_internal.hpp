@@ -20,7 +20,6 @@ struct DecodeWeight {
     int wg_begin;                     // row-wave kernel: first work-group of this weight
     int wrg;                          // row-wave kernel: waves per row-group
     int wg_count;                     // row-wave kernel: work-groups of this weight
-    int cbeg;                         // persistent kernel: first chain of this weight
 };
 
 struct DecodeArgs {
@@ -38,9 +37,6 @@ struct DecodeArgs {
     int ts;                           // tokens per work-group slice (set by the launcher)
     int smax;                         // largest split count of any token (set by the launcher)
     int total_rg;                     // row-groups over all weights (set by the launcher)
-    int total_chains;                 // persistent kernel: (row-group, split) chains of all weights
-    int ps_smin, ps_nrg, ps_rslots, ps_cmax;   // persistent kernel LDS layout (set by the launcher)
-    int ps_q, ps_r;                   // persistent kernel: chains = ps_q * grid + ps_r
 };
 
 struct GemmWeight {
@@ -113,10 +109,24 @@ int device_cus();
 int launch_decode(DecodeArgs &a, bool debug, hipStream_t st);
 // Return 1 (nothing launched) when the shape is outside the kernel's range.
 int launch_rowwave(DecodeArgs &a, hipStream_t st);
-int launch_persist(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
-int launch_gemm2(GemmArgs &a, hipStream_t st);
 int launch_gemm3(GemmArgs &a, hipStream_t st);
+
+// Kernel-selection options (kxw4_set_option): process-wide, read by the
+// launchers. Defaults select the kernels measured fastest; the others keep
+// every kernel reachable for tests and A/B timing. Initialised once per
+// process from the KXW4_* environment variables of the same names.
+enum { kDecodeAuto = 0, kDecodeKParallel = 1, kDecodeRowwave = 2 };
+enum { kGemmAuto = 0, kGemmGeneral = 1 };
+struct Options {
+    int decode_kernel = kDecodeAuto;  // KXW4_DECODE_KERNEL: auto / kparallel / rowwave
+    int rowwave_rpw = 0;              // KXW4_ROWWAVE_RPW: row-groups per work-group, 0 = launcher's plan
+    int rowwave_plain_grid = 0;       // KXW4_ROWWAVE_PLAIN_GRID: 1 = no balanced-round plan
+    int gemm_kernel = kGemmAuto;      // KXW4_GEMM_KERNEL: auto / general
+    int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..9, -1 = cost model
+    int w4a4_tile = -1;               // KXW4_W4A4_TILE: 0..4, -1 = default rule
+};
+const Options &options();
 
 }  // namespace kxw4

@@ -53,6 +53,9 @@ constexpr int kRwMaxWaves = 16;
 // lane (its two masked half MFMAs and scale folds per unit spill at 128)
 constexpr int kRwK16Waves = 8;
 constexpr size_t kRwLdsMax = 160 * 1024;
+// weight tiles in flight per wave (a deeper ring measured slower: its loads
+// at the start delay the activation staging)
+constexpr int kRwRing = 4;
 
 enum { kWfW4 = 0, kWfW8 = 1, kWfK16 = 2 };     // weight format of a row-wave instance
 
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(64 * (WF == kWfK16 ? kRwK16Waves : kRwMaxWaves)) vo
     for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), p);
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (PF * LPT));
+    KXW4_WAIT_VMCNT(PF * LPT);
     const bool ref_block = a.block == 32;
     if (MODE != 0 && UNIT == 32 && ref_block) {
         // per-unit (= per-K32) activation scale and zero-point code sum,
@@ -407,27 +410,21 @@ static int rw_launch(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hip
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
-// pf8: a deeper ring (plain per-token mode only; the general mode keeps 4)
 template <int TT, int UNIT>
-static int rw_mode(const DecodeArgs &a, int mode, bool pf8, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+static int rw_mode(const DecodeArgs &a, int mode, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
     const bool alt2 = a.variant == kVarGemv;
-    if (mode == 0) {
-        if (pf8)
-            return alt2 ? rw_launch<TT, UNIT, 0, true, 8>(a, grid, block, lds, st)
-                        : rw_launch<TT, UNIT, 0, false, 8>(a, grid, block, lds, st);
-        return alt2 ? rw_launch<TT, UNIT, 0, true, 4>(a, grid, block, lds, st)
-                    : rw_launch<TT, UNIT, 0, false, 4>(a, grid, block, lds, st);
-    }
-    return alt2 ? rw_launch<TT, UNIT, 1, true, 4>(a, grid, block, lds, st)
-                : rw_launch<TT, UNIT, 1, false, 4>(a, grid, block, lds, st);
+    if (mode == 0)
+        return alt2 ? rw_launch<TT, UNIT, 0, true, kRwRing>(a, grid, block, lds, st)
+                    : rw_launch<TT, UNIT, 0, false, kRwRing>(a, grid, block, lds, st);
+    return alt2 ? rw_launch<TT, UNIT, 1, true, kRwRing>(a, grid, block, lds, st)
+                : rw_launch<TT, UNIT, 1, false, kRwRing>(a, grid, block, lds, st);
 }
 
 template <int TT>
-static int rw_unit(const DecodeArgs &a, int unit, int mode, bool pf8, dim3 grid, dim3 block, size_t lds,
-                   hipStream_t st) {
-    if (unit == 128) return rw_mode<TT, 128>(a, mode, pf8, grid, block, lds, st);
-    if (unit == 64) return rw_mode<TT, 64>(a, mode, pf8, grid, block, lds, st);
-    return rw_mode<TT, 32>(a, mode, pf8, grid, block, lds, st);
+static int rw_unit(const DecodeArgs &a, int unit, int mode, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+    if (unit == 128) return rw_mode<TT, 128>(a, mode, grid, block, lds, st);
+    if (unit == 64) return rw_mode<TT, 64>(a, mode, grid, block, lds, st);
+    return rw_mode<TT, 32>(a, mode, grid, block, lds, st);
 }
 
 int launch_rowwave(DecodeArgs &a, hipStream_t st) {
@@ -448,7 +445,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // work-groups) row-groups at most, and the LDS request keeps a (k+1)-th
     // work-group off every CU; that plan is kept only when it lowers the
     // most row-groups a CU streams.
-    int rg_total = 0, wrg_max = 1, tiles = 0;
+    int rg_total = 0, wrg_max = 1;
     for (int i = 0; i < a.count; ++i) {
         DecodeWeight &w = a.w[i];
         const int S = w.seg_split[0];
@@ -458,12 +455,10 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         w.wrg = std::min(S, kRwSplitWaves);
         wrg_max = std::max(wrg_max, w.wrg);
         rg_total += w.M / 16;
-        tiles = std::max(tiles, (a.K / kTileK + S - 1) / S);
     }
     const int cus = device_cus();
-    // KXW4_ROWWAVE_RPW=r: r row-groups per work-group (r * min(S, 8) waves)
-    const char *rpe = getenv("KXW4_ROWWAVE_RPW");
-    const int rpw = rpe ? atoi(rpe) : 0;
+    // option rowwave_rpw = r: r row-groups per work-group (r * min(S, 8) waves)
+    const int rpw = options().rowwave_rpw;
     const int max_waves = a.group == 16 ? kRwK16Waves : kRwMaxWaves;
     if (rpw < 0 || rpw * wrg_max > max_waves) return 1;
     int wpw = rpw ? rpw * wrg_max : std::min(kRwWaves, max_waves);
@@ -506,7 +501,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
             wpw = std::min(kRwWaves, max_waves);
             plan(0);
         }
-    } else if (!rpw && !getenv("KXW4_ROWWAVE_DEFAULT_GRID") && wg >= cus && wg % cus != 0) {
+    } else if (!rpw && !options().rowwave_plain_grid && wg >= cus && wg % cus != 0) {
         const int load_plain = (wg + cus - 1) / cus * rmax;
         k = wg / cus;
         plan(k);
@@ -520,31 +515,22 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     if (k) lds = std::max(lds, (size_t)160 * 1024 / (k + 1) + 1024);
     const dim3 block(64 * waves);
     const dim3 grid(wg);
-    // KXW4_ROWWAVE_PF=8 takes the deeper ring (measured slower: more loads in
-    // flight at the start delay the staging)
-    const char *pfe = getenv("KXW4_ROWWAVE_PF");
-    const bool pf8 = pfe && atoi(pfe) == 8 && tiles >= 16;
     if (a.w8) {
         if (unit != 32 || mode != 1) return 1;
         const bool alt2 = a.variant == kVarGemv;
-        if (pf8)
-            return a.T <= 8 ? (alt2 ? rw_launch<8, 32, 1, true, 8, kWfW8>(a, grid, block, lds, st)
-                                    : rw_launch<8, 32, 1, false, 8, kWfW8>(a, grid, block, lds, st))
-                            : (alt2 ? rw_launch<16, 32, 1, true, 8, kWfW8>(a, grid, block, lds, st)
-                                    : rw_launch<16, 32, 1, false, 8, kWfW8>(a, grid, block, lds, st));
         if (a.T <= 8)
-            return alt2 ? rw_launch<8, 32, 1, true, 4, kWfW8>(a, grid, block, lds, st)
-                        : rw_launch<8, 32, 1, false, 4, kWfW8>(a, grid, block, lds, st);
-        return alt2 ? rw_launch<16, 32, 1, true, 4, kWfW8>(a, grid, block, lds, st)
-                    : rw_launch<16, 32, 1, false, 4, kWfW8>(a, grid, block, lds, st);
+            return alt2 ? rw_launch<8, 32, 1, true, kRwRing, kWfW8>(a, grid, block, lds, st)
+                        : rw_launch<8, 32, 1, false, kRwRing, kWfW8>(a, grid, block, lds, st);
+        return alt2 ? rw_launch<16, 32, 1, true, kRwRing, kWfW8>(a, grid, block, lds, st)
+                    : rw_launch<16, 32, 1, false, kRwRing, kWfW8>(a, grid, block, lds, st);
     }
     if (a.group == 16) {
         if (unit != 32 || mode != 1 || a.variant != kVarGemv) return 1;
-        return a.T <= 8 ? rw_launch<8, 32, 1, true, 4, kWfK16>(a, grid, block, lds, st)
-                        : rw_launch<16, 32, 1, true, 4, kWfK16>(a, grid, block, lds, st);
+        return a.T <= 8 ? rw_launch<8, 32, 1, true, kRwRing, kWfK16>(a, grid, block, lds, st)
+                        : rw_launch<16, 32, 1, true, kRwRing, kWfK16>(a, grid, block, lds, st);
     }
-    if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf8, grid, block, lds, st);
-    return rw_unit<16>(a, unit, mode, pf8, grid, block, lds, st);
+    if (a.T <= 8) return rw_unit<8>(a, unit, mode, grid, block, lds, st);
+    return rw_unit<16>(a, unit, mode, grid, block, lds, st);
 }
 
 }  // namespace kxw4

@@ -211,9 +211,9 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void w4a4_kernel(const W4a4Args a
     int st = 0;
     for (int kb = 0; kb < NT; ++kb) {
         const int later = min(NST - 2, NT - 1 - kb);
-        if (NST >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LD));
-        else if (NST >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LD);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        if (NST >= 4 && later >= 2) KXW4_WAIT_VMCNT(2 * LD);
+        else if (NST >= 3 && later >= 1) KXW4_WAIT_VMCNT(LD);
+        else KXW4_WAIT_VMCNT(0);
         lds_sync_after_dma();
         if (kb + NST - 1 < NT) issue(kb + NST - 1, st == 0 ? NST - 1 : st - 1);
         const uint8_t *sb = smem + st * STAGE;
@@ -410,9 +410,8 @@ int launch_w4a4(W4a4Args &a, hipStream_t st) {
     // 196 -> 184 us). The 64 x 160 tile (10 waves, one work-group per CU)
     // balances the cfg2 M=512 grid but measures slower (207 us): with one
     // token block per wave the zero-point weight unpack is no longer shared.
-    // KXW4_W4A4_TILE=0..4 picks one configuration (tests, tuning).
-    const char *cfg = getenv("KXW4_W4A4_TILE");
-    int sel = cfg ? atoi(cfg) : -1;
+    // the w4a4_tile option (0..4) picks one configuration (tests, tuning)
+    int sel = options().w4a4_tile;
     if (sel < 0) {
         const long long tiles = (long long)((a.T + 127) / 128) * ((a.M / 16 + 3) / 4);
         sel = tiles < 2LL * device_cus() ? 4 : 0;

@@ -146,3 +146,26 @@ def test_algorithmic_bytes_match_baseline_table(name):
     want = {"cfg0": 8675328, "cfg1": 92553216, "cfg2_m1": 47405056, "cfg2_m512": 66748416,
             "cfg3": 65945600, "cfg4": 664396800}
     assert workloads.CONFIGS[name].algorithmic_bytes() == want[name]
+
+
+def test_set_option_checks_names_ranges_and_restores():
+    import ctypes as C
+    from knivesysl_xe_amd import ops
+    L = _lib.lib()
+    prev = C.c_int(-99)
+    assert L.kxw4_set_option(b"no_such_option", 0, None) == -1
+    assert L.kxw4_set_option(None, 0, None) == -1
+    assert L.kxw4_set_option(b"decode_kernel", 3, None) == -2
+    assert L.kxw4_set_option(b"gemm3_tile", 10, None) == -2
+    assert L.kxw4_set_option(b"gemm3_tile", -2, None) == -2
+    assert L.kxw4_set_option(b"gemm3_tile", -1, C.byref(prev)) == 0
+    assert prev.value == -1
+    with ops.option("gemm3_tile", 7):
+        assert L.kxw4_set_option(b"gemm3_tile", 7, C.byref(prev)) == 0 and prev.value == 7
+        with ops.option("w4a4_tile", 2):
+            pass
+    assert L.kxw4_set_option(b"gemm3_tile", -1, C.byref(prev)) == 0 and prev.value == -1
+    assert L.kxw4_set_option(b"w4a4_tile", -1, C.byref(prev)) == 0 and prev.value == -1
+    with pytest.raises(_lib.KxError):
+        with ops.option("rowwave_rpw", 17):
+            pass

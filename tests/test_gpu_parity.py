@@ -316,24 +316,20 @@ def test_baseline_cfg4_row_subset():
 
 
 @pytest.fixture
-def kparallel(monkeypatch):
+def kparallel():
     # up to 16 tokens normally run on the row-wave kernel; this keeps the
     # K-parallel decode kernel covered at the decode configurations
-    monkeypatch.setenv("KXW4_DECODE_KERNEL", "kparallel")
+    with ops.option("decode_kernel", 1):
+        yield
 
 
 @pytest.fixture
-def persist(monkeypatch):
-    # the persistent decode kernel runs only when asked for
-    monkeypatch.setenv("KXW4_DECODE_KERNEL", "persist")
-
-
-@pytest.fixture
-def rowwave(monkeypatch):
+def rowwave():
     # per-token shapes with at most 8 tokens and no more row-groups than CUs
     # (cfg0, the small golden cases) normally run on the K-parallel kernel;
     # this keeps the row-wave kernel covered there
-    monkeypatch.setenv("KXW4_DECODE_KERNEL", "rowwave")
+    with ops.option("decode_kernel", 2):
+        yield
 
 
 def test_baseline_cfg0_rowwave(rowwave):
@@ -350,18 +346,19 @@ def test_baseline_config_kparallel(name, kparallel):
     run_config(name)
 
 
-@pytest.mark.parametrize("name", ["cfg0", "cfg1", "cfg2_m1"])
-def test_baseline_config_persist(name, persist):
-    run_config(name)
-
-
-@pytest.mark.parametrize("rpw", ["1", "3", "4", "8"])
-def test_cfg1_rowwave_shapes(rpw, monkeypatch):
+@pytest.mark.parametrize("rpw", [1, 3, 4, 8])
+def test_cfg1_rowwave_shapes(rpw):
     # the row-wave kernel's work-group shape changes only who streams which
     # row-group: every shape gives the same bits (4 = the partial-round shape
     # that the launcher replaces by its balanced plan when left to itself)
-    monkeypatch.setenv("KXW4_ROWWAVE_RPW", rpw)
-    run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
+    with ops.option("rowwave_rpw", rpw):
+        run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
+
+
+def test_cfg1_rowwave_plain_grid():
+    # the plain work-group shape with its partial last round
+    with ops.option("rowwave_plain_grid", 1):
+        run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
 
 
 @pytest.mark.parametrize("rows,K,T,group,block,enc,variant,forced", [
@@ -380,9 +377,9 @@ def test_cfg1_rowwave_shapes(rpw, monkeypatch):
     ([5120], 17408, 1, 64, 32, 1, "gemv", 0),
     ([1024], 2048, 8, 32, 32, 1, "fanout", 0),
 ])
-def test_persist_shapes(rows, K, T, group, block, enc, variant, forced, persist):
-    # the persistent kernel's work split: chain ranges per work-group,
-    # row-groups cut between work-groups, whole and K-split chains
+def test_decode_shapes(rows, K, T, group, block, enc, variant, forced):
+    # decode shapes off the BASELINE grid: fewer row-groups than CUs, mixed
+    # weight heights in one launch, short K, both activation modes
     rng = np.random.default_rng(sum(rows) + K + T)
     wts = [rand_weight(rng, M, K, group, enc) for M in rows]
     x = rng.standard_normal((T, K)).astype(np.float32)
@@ -407,7 +404,7 @@ def test_persist_shapes(rows, K, T, group, block, enc, variant, forced, persist)
                           O.segment_splits(T, c.shape[0], K, None, forced)) for c, sc in wts]
     for i, (y, ref) in enumerate(zip(ys, refs)):
         assert_parity(to_np(y), ref, f"{variant} weight {i} rows={rows[i]}")
-    # a second launch reuses the exchange counters the first one reset
+    # a second launch gives the same bits
     ys2 = ops.gemv_fanout(ws, a) if variant == "fanout" else \
         ops.gemm_fanout(ws, a, torch.float32, forced_splits=forced)
     for y, y2 in zip(ys, ys2):
@@ -415,31 +412,18 @@ def test_persist_shapes(rows, K, T, group, block, enc, variant, forced, persist)
 
 
 @pytest.fixture
-def gemm_general(monkeypatch):
+def gemm_general():
     # the per-token prefill shapes normally run on the large-tile GEMM
     # kernel; this keeps the general GEMM kernel covered on them
-    monkeypatch.setenv("KXW4_GEMM_KERNEL", "general")
+    with ops.option("gemm_kernel", 1):
+        yield
 
 
-@pytest.fixture
-def gemm2(monkeypatch):
-    # and this the smaller-tile LDS-DMA kernel
-    monkeypatch.setenv("KXW4_GEMM_KERNEL", "gemm2")
-
-
-@pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
-def test_baseline_config_gemm2(name, gemm2):
-    run_config(name)
-
-
-def test_baseline_cfg4_rows_gemm2(gemm2):
-    run_config("cfg4", rows=[(0, 256), (17152, 17408)])
-
-
-@pytest.fixture(params=["0", "1", "2", "3", "4", "5", "6", "7", "8", "9"])
-def gemm3_tile(request, monkeypatch):
+@pytest.fixture(params=list(range(10)))
+def gemm3_tile(request):
     # every tile configuration of the large-tile kernel
-    monkeypatch.setenv("KXW4_GEMM3_TILE", request.param)
+    with ops.option("gemm3_tile", request.param):
+        yield request.param
 
 
 @pytest.mark.parametrize("rows,K,T,group", [

@@ -88,10 +88,10 @@ def oracle_w4a4(codes, scales, x, residual=None, out_bf16=False, rows=None):
                      residual=residual, out_bf16=out_bf16, rows=rows)
 
 
-@pytest.fixture(params=["0", "1", "2", "3", "4"])
-def w4a4_tile(request, monkeypatch):
-    monkeypatch.setenv("KXW4_W4A4_TILE", request.param)
-    return request.param
+@pytest.fixture(params=[0, 1, 2, 3, 4])
+def w4a4_tile(request):
+    with ops.option("w4a4_tile", request.param):
+        yield request.param
 
 
 @pytest.mark.parametrize("M,K,T", [(64, 128, 1), (128, 640, 37), (1040, 1024, 300), (256, 5120, 8),
