@@ -253,6 +253,17 @@ int kxw4_gemm_w4a4(const kxw4_weight_t *w, const uint8_t *q4, const float *scale
                    const int32_t *sum, int T, void *y, int y_dtype,
                    const float *residual, void *stream);
 
+/* No counterpart in the reference: an allocation-free x_gemv_w4a8 /
+ * x_gemv_w4a8_add (kernels_dpas.cpp:1662-1680) for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops). x[T][K]
+ * (KXW4_F32 or KXW4_BF16) is quantized per K32 block into a fixed device
+ * array of this library (640 KiB per GPU, held until the process ends), then
+ * projected as kxw4_gemv with the default split plan, plus residual (may be
+ * NULL). Limits: T in [1, 16], K <= 32768 (else -2). Allocates nothing;
+ * calls that overlap on one GPU race on the array. */
+int kxw4_gemv_x_noalloc(const kxw4_weight_t *w, const void *x, int x_dtype, int T, void *y,
+                        int y_dtype, const float *residual, void *stream);
+
 /* ---- TQF1 ingest (host side) ---------------------------------------------
  * The reference's model container (tqf_loader.cpp:393-626): kxw4_tqf_open
  * validates the header as the reference does (BF16 non-quant tensors, dense

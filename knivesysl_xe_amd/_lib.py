@@ -61,6 +61,7 @@ SIGNATURES = {
     "kxw4_gemm": (I, [WP, AP, P, I, P, C.POINTER(I), I, I, P]),
     "kxw4_gemm_fanout": (I, [C.POINTER(WP), C.POINTER(P), I, AP, I, C.POINTER(I), I, I, P]),
     "kxw4_gemm_w4a4": (I, [WP, P, P, P, I, P, I, P, P]),
+    "kxw4_gemv_x_noalloc": (I, [WP, P, I, I, P, I, P, P]),
     "kxw4_tqf_open": (I, [C.c_char_p, C.POINTER(P)]),
     "kxw4_tqf_close": (None, [P]),
     "kxw4_tqf_count": (I, [P]),
