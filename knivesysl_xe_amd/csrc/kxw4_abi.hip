@@ -22,11 +22,12 @@ struct OptionDesc {
 
 const OptionDesc kOptions[] = {
     {"decode_kernel", &Options::decode_kernel, kDecodeAuto, kDecodeRowwave},
-    {"rowwave_rpw", &Options::rowwave_rpw, 0, 16},
-    {"rowwave_plain_grid", &Options::rowwave_plain_grid, 0, 1},
+    {"rowwave_spw", &Options::rowwave_spw, 0, 16},
     {"gemm_kernel", &Options::gemm_kernel, kGemmAuto, kGemmGeneral},
     {"gemm3_tile", &Options::gemm3_tile, -1, 9},
     {"w4a4_tile", &Options::w4a4_tile, -1, 4},
+    {"rowwave_ring", &Options::rowwave_ring, 0, 8},
+    {"rowwave_k", &Options::rowwave_k, 0, 64},
 };
 
 // The environment is read once, when the library first selects a kernel.
@@ -42,8 +43,9 @@ Options from_env() {
         const int v = atoi(e);
         if (v >= lo && v <= hi) dst = v;
     };
-    num("KXW4_ROWWAVE_RPW", 0, 16, o.rowwave_rpw);
-    num("KXW4_ROWWAVE_PLAIN_GRID", 0, 1, o.rowwave_plain_grid);
+    num("KXW4_ROWWAVE_SPW", 0, 16, o.rowwave_spw);
+    num("KXW4_ROWWAVE_RING", 0, 8, o.rowwave_ring);
+    num("KXW4_ROWWAVE_K", 0, 64, o.rowwave_k);
     if (const char *e = getenv("KXW4_GEMM_KERNEL"))
         if (!strcmp(e, "general")) o.gemm_kernel = kGemmGeneral;
     num("KXW4_GEMM3_TILE", -1, 9, o.gemm3_tile);

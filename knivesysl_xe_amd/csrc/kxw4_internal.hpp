@@ -15,11 +15,8 @@ struct DecodeWeight {
     const uint16_t *scales;
     void *y;
     int M;
-    int rg_begin;                     // first work-group (row-group) of this weight (set by the launcher)
+    int rg_begin;                     // first row-group of this weight over all weights (set by the launcher)
     int seg_split[kMaxSegments];      // split count per packed segment
-    int wg_begin;                     // row-wave kernel: first work-group of this weight
-    int wrg;                          // row-wave kernel: waves per row-group
-    int wg_count;                     // row-wave kernel: work-groups of this weight
 };
 
 struct DecodeArgs {
@@ -37,6 +34,10 @@ struct DecodeArgs {
     int ts;                           // tokens per work-group slice (set by the launcher)
     int smax;                         // largest split count of any token (set by the launcher)
     int total_rg;                     // row-groups over all weights (set by the launcher)
+    // row-wave kernel plan (set by its launcher): split count, waves per
+    // slice, slices per work-group, 8-row halves over all weights, most
+    // row-groups one work-group touches
+    int rw_S, rw_wrg, rw_spw, rw_halves, rw_grmax;
 };
 
 struct GemmWeight {
@@ -121,8 +122,9 @@ enum { kDecodeAuto = 0, kDecodeKParallel = 1, kDecodeRowwave = 2 };
 enum { kGemmAuto = 0, kGemmGeneral = 1 };
 struct Options {
     int decode_kernel = kDecodeAuto;  // KXW4_DECODE_KERNEL: auto / kparallel / rowwave
-    int rowwave_rpw = 0;              // KXW4_ROWWAVE_RPW: row-groups per work-group, 0 = launcher's plan
-    int rowwave_plain_grid = 0;       // KXW4_ROWWAVE_PLAIN_GRID: 1 = no balanced-round plan
+    int rowwave_spw = 0;              // KXW4_ROWWAVE_SPW: row slices per work-group, 0 = launcher's plan
+    int rowwave_ring = 0;             // KXW4_ROWWAVE_RING: weight tiles in flight per wave, 8 (else 4)
+    int rowwave_k = 0;                // KXW4_ROWWAVE_K: work-groups per CU, 0 = launcher's plan
     int gemm_kernel = kGemmAuto;      // KXW4_GEMM_KERNEL: auto / general
     int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..9, -1 = cost model
     int w4a4_tile = -1;               // KXW4_W4A4_TILE: 0..4, -1 = default rule

@@ -346,19 +346,19 @@ def test_baseline_config_kparallel(name, kparallel):
     run_config(name)
 
 
-@pytest.mark.parametrize("rpw", [1, 3, 4, 8])
-def test_cfg1_rowwave_shapes(rpw):
-    # the row-wave kernel's work-group shape changes only who streams which
-    # row-group: every shape gives the same bits (4 = the partial-round shape
-    # that the launcher replaces by its balanced plan when left to itself)
-    with ops.option("rowwave_rpw", rpw):
+@pytest.mark.parametrize("spw,ring", [(1, 4), (2, 4), (3, 8), (4, 8), (8, 4)])
+def test_cfg1_rowwave_shapes(spw, ring):
+    # the row-wave kernel's slicing (rows per wave, one or two 16-row
+    # windows) and ring depth change only who streams which rows: every shape
+    # gives the same bits
+    with ops.option("rowwave_spw", spw), ops.option("rowwave_ring", ring):
         run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
 
 
-def test_cfg1_rowwave_plain_grid():
-    # the plain work-group shape with its partial last round
-    with ops.option("rowwave_plain_grid", 1):
-        run_config("cfg1", rows=[(0, 512), (8192, 8704), (16896, 17408)])
+@pytest.mark.parametrize("ring", [4, 8])
+def test_cfg2_m1_rowwave_ring(ring):
+    with ops.option("rowwave_ring", ring):
+        run_config("cfg2_m1")
 
 
 @pytest.mark.parametrize("rows,K,T,group,block,enc,variant,forced", [
