@@ -286,26 +286,86 @@ def measure_w8a8(steps, warmup, eager=False, rows=LM_HEAD_ROWS, K=5120, T=8):
     return res
 
 
-def cpu_baseline(cfg, budget_s=10.0):
-    """The oracle on the host cores over repeated full passes of `cfg`."""
+def cpu_info():
+    """CPU model name, the host's logical CPUs and those this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return model, os.cpu_count(), usable
+
+
+def cpu_time_config(cfg, budget_s):
+    """The oracle on the host cores for one config: whole weights for the
+    decode shapes, else a row subset sized so a pass takes about a tenth of
+    the budget; one warm-up pass, then timed passes until the budget is spent;
+    the median pass gives GB/s and GOPS of that subset's algorithmic work
+    (codes + scales of the rows, all activations, the rows' outputs)."""
     from oracle import oracle as O
     from knivesysl_xe_amd import workloads
-    O.build()
     inp = workloads.generate(cfg, 0)
     q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(inp.x_bf16), 0)
     splits = [O.segment_splits(cfg.tokens, c.shape[0], cfg.K, cfg.offsets) for c in inp.codes]
-    reps, t0 = 0, time.perf_counter()
-    while True:
+
+    def one_pass(rows):
+        t0 = time.perf_counter()
         for c, sc, sp in zip(inp.codes, inp.scales, splits):
-            O.project(c, sc, cfg.group, 0, q, s, sm, 0, O.VAR_GEMM, sp, out_bf16=cfg.out_bf16)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": cfg.algorithmic_bytes() * reps / el / 1e9, "unit": "GB/s",
-            "cores": O.num_threads(), "kind": "port",
-            "sample": f"{reps} full {cfg.name} passes (both weights, all 8 tokens) in {el:.1f} s; "
-                      "scalar C++ oracle, OpenMP over output rows"}
+            r = min(rows, c.shape[0])
+            O.project(c, sc, cfg.group, 0, q, s, sm, 0, O.VAR_GEMM, sp, out_bf16=cfg.out_bf16,
+                      rows=(0, r))
+        return time.perf_counter() - t0
+
+    M = max(c.shape[0] for c in inp.codes)
+    if cfg.tokens <= 16:
+        rows = M                                         # decode shapes: whole weights
+        one_pass(rows)                                   # warm-up
+    else:
+        rows = min(M, 256)
+        t = one_pass(rows)                               # warm-up and calibration
+        rows = int(min(M, max(16, rows * (budget_s / 10) / max(t, 1e-6))) // 16 * 16) or 16
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < 50):
+        times.append(one_pass(rows))
+    per = float(np.median(times))
+    nr = sum(min(rows, c.shape[0]) for c in inp.codes)
+    nbytes = nr * cfg.K // 2 + nr * (cfg.K // cfg.group) * 2 + cfg.tokens * cfg.K * 2 + \
+        cfg.tokens * nr * (2 if cfg.out_bf16 else 4)
+    ops = 2 * cfg.tokens * nr * cfg.K
+    return {"GBps": nbytes / per / 1e9, "GOPS": ops / per / 1e9, "rows": nr,
+            "rows_total": sum(c.shape[0] for c in inp.codes), "passes": len(times),
+            "s_per_pass": per}
+
+
+def cpu_baseline(head, names, budget_s=3.0):
+    """The oracle (scalar C++ restatement of the reference arithmetic, OpenMP
+    over output rows) on the host cores for the headline and each config."""
+    from oracle import oracle as O
+    from knivesysl_xe_amd import workloads
+    O.build()
+    model, nproc, usable = cpu_info()
+    per = {}
+    for name in dict.fromkeys(["cfg1"] + list(names)):
+        per[name] = cpu_time_config(workloads.CONFIGS[name], budget_s)
+        log(f"cpu {name}: {per[name]['GBps']:.2f} GB/s, {per[name]['GOPS']:.1f} GOPS "
+            f"({per[name]['rows']}/{per[name]['rows_total']} rows, {per[name]['passes']} passes)")
+    h = per["cfg1"]
+    return {"value": h["GBps"], "unit": "GB/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"cfg1 whole weights (both, all 8 tokens), median of {h['passes']} passes; "
+                      "other configs on the row subsets listed; scalar C++ oracle, OpenMP over "
+                      "output rows",
+            "cpu_model": model, "nproc": nproc, "usable_cpus": usable,
+            "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                        for k, v in per.items()}}
 
 
 def calibration_copy(mib):
@@ -368,25 +428,42 @@ def machine_probes(head_bytes):
     return out
 
 
-def read_traffic(name):
+def source_digest(files):
+    """sha256 over the kernel sources a traffic figure was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in files:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+HEADLINE_SOURCES = ["knivesysl_xe_amd/csrc/kxw4_rowwave.hip", "knivesysl_xe_amd/csrc/kxw4_device.hpp",
+                    "knivesysl_xe_amd/csrc/kxw4_internal.hpp"]
+
+
+def read_traffic(name, sources):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any:
     fetch_kib * fetch_cal + write_kib * write_cal, where each factor is the
-    known size of a plain copy over what the same counter read for it."""
+    known size of a plain copy over what the same counter read for it. The
+    summary names the sha256 of the kernel sources it was measured on; when
+    they have changed since, the figure is stale and (None, reason) is
+    returned instead."""
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
     if not os.path.exists(path):
-        return None
+        return None, "no counter summary"
     vals = {}
     for line in open(path):
         if "=" in line and not line.lstrip().startswith("#"):
             k, v = line.split("=", 1)
-            try:
-                vals[k.strip()] = float(v.split()[0])
-            except ValueError:
-                pass
+            vals[k.strip()] = v.split()[0] if v.split() else ""
+    if vals.get("source_sha256") != source_digest(sources):
+        return None, "counter summary measured on other kernel sources"
     try:
-        return int((vals["fetch_kib"] * vals["fetch_cal"] + vals["write_kib"] * vals["write_cal"]) * 1024)
-    except KeyError:
-        return None
+        kib = float(vals["fetch_kib"]) * float(vals["fetch_cal"]) + float(vals["write_kib"]) * float(vals["write_cal"])
+    except (KeyError, ValueError):
+        return None, "counter summary incomplete"
+    return int(kib * 1024), f"profiles/traffic_{name}.txt"
 
 
 def main():
@@ -401,7 +478,8 @@ def main():
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
     ap.add_argument("--no-probes", action="store_true", help="skip the MFMA / HBM read probes")
     ap.add_argument("--extra-steps", type=int, default=50)
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-budget", type=float, default=3.0,
+                    help="seconds of CPU-baseline timing per config")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a graph replay (for counter runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -449,8 +527,9 @@ def main():
     if args.copy_mib:
         calibration_copy(args.copy_mib)
     log("cpu baseline (oracle on host cores)")
-    cpu = cpu_baseline(head, args.cpu_budget)
+    cpu = cpu_baseline(head, ["cfg0", "cfg2_m1", "cfg2_m512", "cfg3", "cfg4"], args.cpu_budget)
     per = r["kernel_us"] / 1e6
+    traffic, traffic_src = read_traffic("cfg1", HEADLINE_SOURCES)
     out = {
         "metric": "W4A8 GEMV HBM GB/s (M=1,8) + prefill GEMM int8 TOPS, % of MI355X roofline",
         "value": round(r["GBps"], 2),
@@ -470,7 +549,7 @@ def main():
                    "tokens": 8, "K": 5120, "N": 34816, "group": 128, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(r["GBps"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(r["GBps"] / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic("cfg1")},
+                     "traffic": traffic, "traffic_source": traffic_src},
         "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()},
         "bit_exact_vs_oracle": r["bit_exact_vs_oracle_rows0_512"],
         "probes": None if probes is None else dict(
