@@ -99,8 +99,9 @@ const char *kxw4_error_string(int code);
  * the kernels measured fastest and the results are the same bits either way.
  *   decode_kernel      0 auto, 1 K-parallel kernel only, 2 row-wave kernel
  *                      wherever it applies
- *   rowwave_rpw        row-groups per row-wave work-group, 0 = launcher's plan
- *   rowwave_plain_grid 1 = plain work-groups even with a partial last round
+ *   rowwave_spw        row slices per row-wave work-group, 0 = launcher's plan
+ *   rowwave_k          row-wave work-groups per CU, 0 = launcher's plan
+ *   rowwave_ring       8 = eight weight tiles in flight per wave (else 4)
  *   gemm_kernel        0 auto, 1 the general GEMM for every prefill shape
  *   gemm3_tile         -1 cost model, 0..9 one 32x32x32 GEMM tile
  *   w4a4_tile          -1 default rule, 0..4 one W4A4 GEMM tile
