@@ -15,13 +15,17 @@
 //     the next block's MFMAs;
 //   * the unpacked weight operands of a step stay in registers, the
 //     activation operands stream one 32-token block at a time;
-//   * the work-group is WMW x WNW waves; each packed weight tile is unpacked
-//     by one wave only;
+//   * the work-group is WMW x WNW waves; a wave unpacks the packed weight
+//     tiles of its own row blocks;
 //   * per 128-K step the activation tile, the packed weight tiles and the
-//     FP16 scales reach LDS through direct global->LDS loads into a ring of
-//     NST stages; every wave issues the same number of loads per stage, so
-//     one vmcnt retires a stage, and one barrier per step both publishes the
-//     stage and frees the one refilled next.
+//     FP16 scales reach LDS through buffer loads straight into LDS, into a
+//     ring of NST stages; every wave issues the same number of loads per
+//     stage, so one vmcnt retires a stage, and one barrier per step both
+//     publishes the next stage and frees the one refilled next;
+//   * the pipeline runs across steps: the barrier sits before a step's last
+//     block, the next step's first operands are read during that block, and
+//     the last block's updates run under the next step's first MFMAs, so no
+//     step starts or ends with the matrix core idle.
 //
 // Operand K sets: the packed tile keeps the 16x16x64 lane order (lane n+16g
 // holds row n, K slots of lane group g of both 64-K halves). MFMA c of a step
@@ -45,6 +49,10 @@ namespace kxw4 {
 constexpr int kG3GroupTT = 4;      // token tiles per raster group
 
 #define KXW4_G3_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Word 3 of a buffer descriptor for untyped loads: data format 32 (a zero
+// format reads zeros), no swizzle, no index.
+constexpr int kBufWord3 = 0x00020000;
 
 template <int TA, int TB, int WMW, int WNW, int UNIT>
 struct G3Shape {
@@ -132,53 +140,79 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WNW, wn = wave % WNW;
 
-    // ---- load issue: per-lane 32-bit source offsets that do not depend on
-    // the K step (the launcher keeps T*K and M*K/2 below 2^31) ----
-    uint32_t aoffs[S::A_LOADS];
-#pragma unroll
-    for (int i = 0; i < S::A_LOADS; ++i) {
-        const int p = ((wave + NW * i) % S::A_CHUNKS) * 64 + lane;            // granule this lane fills
-        const int t = 2 * (p >> 4) + ((p >> 3) & 1);
-        const int c16 = (p & 7) ^ ((t >> 1) & 7);
-        const int tg = min(t0 + t, T - 1);                    // rows past T: never stored
-        aoffs[i] = (uint32_t)tg * K + c16 * 16;
-    }
-    uint32_t boffs[S::B_LOADS];
-#pragma unroll
-    for (int i = 0; i < S::B_LOADS; ++i) {
-        const int rg = min(rg0 + (wave + NW * i) % BNG, RG - 1);      // row-groups past M: never stored
-        boffs[i] = (uint32_t)rg * NT * kTileBytes + lane * 16;
-    }
-    // scale granule gi = (j * UPS + u) * 2 + half of this wave's slice
-    uint32_t soff;
-    {
-        const int gi = (wave * S::S_LANES + min(lane, S::S_LANES - 1)) % S::S_TOTAL;
+    // ---- load issue: buffer loads straight into LDS. A wave fills whole
+    // 1 KB chunks, so the rows of each of its loads are the same for every
+    // lane: a buffer descriptor per load holds the first row and the bytes of
+    // the rows that exist, and rows past T (activations) or M (weights) read
+    // as zero through the descriptor's range check (they are never stored).
+    // The lane part of each offset is one 32-bit VGPR per kind of load, the K
+    // step goes in the scalar offset (the launcher keeps T*K and M*K/2 below
+    // 2^31). Activation chunk ch holds tile rows 8ch..8ch+7: lane l fills
+    // row 8ch + 2(l/16) + (l/8)%2, 16-byte chunk (l%8) ^ ((4ch + l/16) % 8),
+    // and a wave's chunks all have the parity of the wave ----
+    static_assert(NW % 2 == 0 && S::A_CHUNKS % 2 == 0, "one activation lane offset per wave");
+    // Lane parts of the offsets: activations, weights, and scale granule
+    // gi = (j * UPS + u) * 2 + half of this wave's slice (a slice never
+    // wraps; row-groups past M repeat the last one).
+    auto lane_offsets = [&](int ln, uint32_t &al, uint32_t &bl, uint32_t &so) {
+        al = (uint32_t)(2 * (ln >> 4) + ((ln >> 3) & 1)) * K +
+             (uint32_t)(((ln & 7) ^ ((4 * (wave & 1) + (ln >> 4)) & 7)) * 16);
+        bl = ln * 16;
+        const int gi = (wave * S::S_LANES) % S::S_TOTAL + min(ln, S::S_LANES - 1);
         const int j = gi / (2 * UPS), u = (gi >> 1) % UPS, half = gi & 1;
         const int rg = min(rg0 + j, RG - 1);
-        soff = ((uint32_t)rg * G + u) * 16 + half * 8;
-    }
-    // (the DMA builtin takes a generic void pointer: with a typed pointer the
-    // host compilation pass drops the kernel without a diagnostic)
+        so = (((uint32_t)rg * G + u) * 16 + half * 8) * 2;
+    };
+    // With three waves per SIMD the registers are short: the lane parts are
+    // recomputed at each issue instead of held across the K loop.
+    constexpr bool kLaneRecompute = OCC >= 3;
+    uint32_t a_lane0 = 0, b_lane0 = 0, soff0 = 0;
+    if constexpr (!kLaneRecompute) lane_offsets(lane, a_lane0, b_lane0, soff0);
+    // The descriptors are built at each issue from scalars (a few SALU
+    // operations): held in arrays, of descriptors or of their base pointers,
+    // they make the host compilation pass drop the kernel without a
+    // diagnostic. The base pointers are pinned in SGPRs, or the compiler
+    // reloads them from the kernel arguments at every issue, and a pending
+    // scalar load turns every LDS wait in the loop into lgkmcnt(0).
+    const int8_t *qg = a.q;
+    const uint8_t *cg = W.codes;
+    const uint16_t *sg = W.scales;
+    asm volatile("" : "+s"(qg), "+s"(cg), "+s"(sg));
     auto issue = [&](int kb, int st) {
+        uint32_t a_lane = a_lane0, b_lane = b_lane0, soff = soff0;
+        if constexpr (kLaneRecompute) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));          // (not loop-invariant, so not hoisted)
+            lane_offsets(ln, a_lane, b_lane, soff);
+        }
         uint8_t *base = smem + st * STAGE;
-        const int8_t *qk = a.q + (size_t)kb * kTileK;
-        const uint8_t *wk = W.codes + (size_t)kb * kTileBytes;
 #pragma unroll
-        for (int i = 0; i < S::A_LOADS; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(qk + aoffs[i]),
-                                             KXW4_G3_LDS(base + ((wave + NW * i) % S::A_CHUNKS) * 1024), 16, 0, 0);
+        for (int i = 0; i < S::A_LOADS; ++i) {
+            const int r = t0 + 8 * ((wave + NW * i) % S::A_CHUNKS);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                __builtin_amdgcn_make_buffer_rsrc((void *)(qg + (size_t)min(r, T - 1) * K), 0, max(T - r, 0) * K, kBufWord3),
+                KXW4_G3_LDS(base + ((wave + NW * i) % S::A_CHUNKS) * 1024),
+                16, a_lane, kb * kTileK, 0, 0);
+        }
 #pragma unroll
-        for (int i = 0; i < S::B_LOADS; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(wk + boffs[i]),
-                                             KXW4_G3_LDS(base + A_BYTES + ((wave + NW * i) % BNG) * 1024), 16, 0, 0);
+        for (int i = 0; i < S::B_LOADS; ++i) {
+            const int rg = rg0 + (wave + NW * i) % BNG;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                __builtin_amdgcn_make_buffer_rsrc((void *)(cg + (size_t)min(rg, RG - 1) * NT * kTileBytes), 0,
+                                                  rg < RG ? NT * kTileBytes : 0, kBufWord3),
+                KXW4_G3_LDS(base + A_BYTES + ((wave + NW * i) % BNG) * 1024),
+                16, b_lane, kb * kTileBytes, 0, 0);
+        }
         // lanes past the wave's granules are masked off; the load still
         // counts once in vmcnt
         if (lane < S::S_LANES)
-            __builtin_amdgcn_global_load_lds((const void *)(W.scales + (size_t)kb * UPS * 16 + soff),
-                                             KXW4_G3_LDS(base + A_BYTES + B_BYTES + (wave * S::S_LANES) % S::S_TOTAL * 16),
-                                             16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(__builtin_amdgcn_make_buffer_rsrc((void *)sg, 0, RG * G * 32, kBufWord3),
+                                                     KXW4_G3_LDS(base + A_BYTES + B_BYTES + (wave * S::S_LANES) % S::S_TOTAL * 16),
+                                                     16, soff, kb * UPS * 32, 0, 0);
         // with the first stage, the tile's token scales (64 per wave); the
         // later stages' loads are all younger, so the first wait retires it
+        // (the DMA builtin takes a generic void pointer: with a typed pointer
+        // the host compilation pass drops the kernel without a diagnostic)
         if (kb == 0 && wave * 64 < BM)
             __builtin_amdgcn_global_load_lds((const void *)(a.ascale + min(t0 + wave * 64 + lane, T - 1)),
                                              KXW4_G3_LDS(smem + S::template body_bytes<NST>() + wave * 256), 4, 0, 0);
@@ -198,6 +232,11 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     const int jrel0 = wn * 2 * TB + (m32 >> 4);
     const int boff = A_BYTES + jrel0 * kTileBytes + (kg * 16 + (m32 & 15)) * 16;
     const int soff_lds = A_BYTES + B_BYTES + (jrel0 * UPS * 16 + (m32 & 15)) * 2;
+    // the same offsets inside the current step's stage, moved on each step
+    // (so a read needs no address arithmetic)
+    int ast[4], bst = boff, sst = soff_lds;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ast[c] = aoff[c];
 
     float f[TA][TB][16];
 #pragma unroll
@@ -207,111 +246,222 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
 #pragma unroll
             for (int r = 0; r < 16; ++r) f[i][j][r] = 0.0f;
 
-    // Ring of NST stages; stage k % NST is issued at the top of step
-    // k - (NST - 1). At the top of step k this wave's loads of steps
-    // k .. k + NST - 2 may be outstanding; vmcnt(LOADS * later) retires step
-    // k's, where `later` counts the stages issued after it. The barrier then
-    // publishes every wave's loads and guarantees that stage (k - 1) % NST,
-    // refilled next, is no longer read.
+    // Ring of NST stages; step k's loads go to stage k % NST. A wave reaches
+    // arrive(k) just before the last 32x32 block of step k - 1 (before the
+    // loop for k = 0): vmcnt retires its own loads of step k (those of the
+    // stages issued after it may stay in flight), lgkmcnt(0) completes its
+    // reads of step k - 1, whose operands are all in registers by then, and
+    // the barrier makes both hold for every wave. Step k - 1's stage is then
+    // free and takes step k - 1 + NST; the first operands of step k are read
+    // while the last block of step k - 1 runs.
     static_assert(NST >= 2 && NST <= 4, "two to four stages");
     constexpr int LD = S::LOADS;
     static_assert(LD * (NST - 2) <= 63, "vmcnt field");
-#pragma unroll
-    for (int s = 0; s < NST - 1; ++s)
-        if (s < NT) issue(s, s);
-    int st = 0;
-    for (int kb = 0; kb < NT; ++kb) {
-        const int later = min(NST - 2, NT - 1 - kb);
+    auto arrive = [&](int k) {
+        const int later = min(NST - 2, NT - 1 - k);
         if (NST >= 4 && later >= 2) KXW4_WAIT_VMCNT(2 * LD);
         else if (NST >= 3 && later >= 1) KXW4_WAIT_VMCNT(LD);
         else KXW4_WAIT_VMCNT(0);
         lds_sync_after_dma();
-        if (kb + NST - 1 < NT) issue(kb + NST - 1, st == 0 ? NST - 1 : st - 1);
-        const uint8_t *sb = smem + st * STAGE;
-        // weight operands of the step: block jb, MFMA c = 2h + half
-        v4i B[TB][4];
-        float w[TB][UPS];
+    };
+    // operand reads from a stage (block jb's packed weight dwords, MFMA
+    // c = 2h + half; its FP16 group scales; token block ib's activations)
+    // (d: 0 for the current stage, else the byte distance to the next)
+    auto read_b = [&](int d, int jb, v4u (&wd)[2]) {
 #pragma unroll
-        for (int jb = 0; jb < TB; ++jb) {
+        for (int h = 0; h < 2; ++h)
+            wd[h] = *reinterpret_cast<const v4u *>(smem + bst + d + jb * 2 * kTileBytes + h * 512);
+    };
+    auto unpack_b = [&](const v4u (&wd)[2], v4i (&Bj)[4]) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const v4u wd = *reinterpret_cast<const v4u *>(sb + boff + jb * 2 * kTileBytes + h * 512);
-                B[jb][2 * h] = unpack_k64(wd.x, wd.y);
-                B[jb][2 * h + 1] = unpack_k64(wd.z, wd.w);
-            }
+        for (int h = 0; h < 2; ++h) {
+            Bj[2 * h] = unpack_k64(wd[h].x, wd[h].y);
+            Bj[2 * h + 1] = unpack_k64(wd[h].z, wd[h].w);
+        }
+    };
+    auto read_w = [&](int d, float (&wv)[TB][UPS]) {
+#pragma unroll
+        for (int jb = 0; jb < TB; ++jb)
 #pragma unroll
             for (int u = 0; u < UPS; ++u)
-                w[jb][u] = half_bits_to_float(
-                    *reinterpret_cast<const uint16_t *>(sb + soff_lds + (jb * 2 * UPS + u) * 32));
+                wv[jb][u] = half_bits_to_float(
+                    *reinterpret_cast<const uint16_t *>(smem + sst + d + (jb * 2 * UPS + u) * 32));
+    };
+    auto read_a = [&](int d, int ib, v4i (&A)[4]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) A[c] = *reinterpret_cast<const v4i *>(smem + ast[c] + d + ib * 4096);
+    };
+
+    // Software pipeline over the 32x32 blocks of all steps (row block jb
+    // fastest within a step): block b issues its MFMAs interleaved with the
+    // chain updates of the block before it (at a step's first block, the
+    // previous step's last), so the updates run while the matrix core works.
+    // Within a step, token block ib + 1's activations are read at block
+    // (ib, 0) and weight block jb + 1 at block (0, jb), one block ahead.
+    constexpr int NB = TA * TB;
+    v4i B[TB][4];
+    v4u raw[2];                        // TB = 1: the next step's packed tile
+    float w[TB][UPS], wnext[TB][UPS], wlast[UPS];
+    v4i Acur[4], Anext[4];
+    // acc[slot][u]: the 64-K group u of a block (one group per block at
+    // group 128, where MFMAs 0-3 chain into acc[.][0]; at group 64 the
+    // first 64-K half is MFMAs 0 and 2, the second 1 and 3); consecutive
+    // blocks alternate slots across steps too
+    v16i acc[2][UPS];
+    const v16i zero = {};
+    auto read_next_step = [&](int d) {
+        if constexpr (TB == 1) {
+            read_b(d, 0, raw);
+        } else {
+            v4u wd[2];
+            read_b(d, 0, wd);
+            unpack_b(wd, B[0]);
         }
-        // Software pipeline over the step's TA*TB blocks (row block jb
-        // fastest): stage b issues block b's MFMAs interleaved with block
-        // b-1's chain updates, so the updates run while the matrix core
-        // works. The activation operands of the next token block are read
-        // during the last stage of the current one.
-        constexpr int NB = TA * TB;
-        v4i Acur[4], Anext[4];
+        read_w(d, wnext);
+        read_a(d, 0, Anext);
+    };
+    auto update = [&](int ib, int jb, const v16i (&p)[UPS], const float (&wv)[UPS]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) Acur[c] = *reinterpret_cast<const v4i *>(sb + aoff[c]);
-        // acc[slot][u]: the 64-K group u of a block (one group per block
-        // at group 128, where MFMAs 0-3 chain into acc[.][0]; at group 64
-        // the first 64-K half is MFMAs 0 and 2, the second 1 and 3)
-        v16i acc[2][UPS];
-        const v16i zero = {};
-        auto update = [&](int b) {
+        for (int u = 0; u < UPS; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                f[ib][jb][r] = __builtin_fmaf((float)p[u][r], wv[u], f[ib][jb][r]);
+    };
+    // LDS reads block b issues ahead of its MFMAs
+    auto ds_reads = [](int b) {
+        const int ib = b / TB, jb = b % TB;
+        if (b == NB - 1) return 2 + TB * UPS + 4;
+        return (jb == 0 && ib + 1 < TA ? 4 : 0) + (ib == 0 && jb + 1 < TB ? 2 : 0);
+    };
+    // (the group size must be a literal; the block loop is unrolled, so the
+    // switch folds)
+    auto ds_first = [](int n) {
+        switch (n) {
+        case 2: __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); break;
+        case 4: __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); break;
+        case 6: __builtin_amdgcn_sched_group_barrier(0x100, 6, 0); break;
+        case 7: __builtin_amdgcn_sched_group_barrier(0x100, 7, 0); break;
+        case 8: __builtin_amdgcn_sched_group_barrier(0x100, 8, 0); break;
+        case 10: __builtin_amdgcn_sched_group_barrier(0x100, 10, 0); break;
+        default: break;
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s)
+        if (s < NT) issue(s, s);
+    arrive(0);
+    if (NST - 1 < NT) issue(NST - 1, NST - 1);
+    read_next_step(0);
+    // (complete here: the wait pass would otherwise assume them pending at
+    // the loop head and wait on every step's first MFMA)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    // step 0's first block "updates" the last block of no step: a zero
+    // product at a zero scale leaves its +0 chain unchanged
+#pragma unroll
+    for (int u = 0; u < UPS; ++u) acc[1][u] = zero;
+#pragma unroll
+    for (int jb = 0; jb < TB; ++jb)
+#pragma unroll
+        for (int u = 0; u < UPS; ++u) w[jb][u] = 0.0f;
+
+    int st = 0;
+    auto step = [&](const int kb, auto par) {
+        constexpr int PAR = decltype(par)::value;
+        const int stn = st == NST - 1 ? 0 : st + 1;
+        const int dn = (stn - st) * STAGE;
+        const bool more = kb + 1 < NT;
+#pragma unroll
+        for (int u = 0; u < UPS; ++u) wlast[u] = w[TB - 1][u];
+#pragma unroll
+        for (int jb = 0; jb < TB; ++jb)
+#pragma unroll
+            for (int u = 0; u < UPS; ++u) w[jb][u] = wnext[jb][u];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
             const int ib = b / TB, jb = b % TB;
-#pragma unroll
-            for (int u = 0; u < UPS; ++u) {
-                const v16i &p = acc[b & 1][u];
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    f[ib][jb][r] = __builtin_fmaf((float)p[r], w[jb][u], f[ib][jb][r]);
+            const int slot = (PAR * NB + b) & 1;
+            if (b == NB - 1) {
+                if (more) {
+                    arrive(kb + 1);
+                    if (kb + NST < NT) issue(kb + NST, st);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-        };
+            if (jb == 0) {
 #pragma unroll
-        for (int b = 0; b <= NB; ++b) {
-            if (b < NB) {
-                const int ib = b / TB, jb = b % TB;
-                if (jb == 0 && ib > 0) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) Acur[c] = Anext[c];
-                }
-                if (jb == TB - 1 && ib + 1 < TA) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        Anext[c] = *reinterpret_cast<const v4i *>(sb + aoff[c] + (ib + 1) * 4096);
-                }
-                if constexpr (UNIT == 128) {
-                    v16i &p = acc[b & 1][0];
-                    p = mfma32(Acur[0], B[jb][0], zero);
-                    p = mfma32(Acur[1], B[jb][1], p);
-                    p = mfma32(Acur[2], B[jb][2], p);
-                    p = mfma32(Acur[3], B[jb][3], p);
-                } else {
-                    static_assert(UNIT == 64, "per-token mode has unit = group in {64, 128}");
-                    v16i &p0 = acc[b & 1][0];
-                    v16i &p1 = acc[b & 1][UPS - 1];
-                    p0 = mfma32(Acur[0], B[jb][0], zero);
-                    p1 = mfma32(Acur[1], B[jb][1], zero);
-                    p0 = mfma32(Acur[2], B[jb][2], p0);
-                    p1 = mfma32(Acur[3], B[jb][3], p1);
+                for (int c = 0; c < 4; ++c) Acur[c] = Anext[c];
+            }
+            if constexpr (TB == 1) {
+                if (b == 0) unpack_b(raw, B[0]);
+            }
+            if (b == NB - 1) {
+                // the next step's first operands (after the last step: a
+                // harmless read of a stale stage)
+                read_next_step(dn);
+            } else {
+                if (jb == 0 && ib + 1 < TA) read_a(0, ib + 1, Anext);
+                if (ib == 0 && jb + 1 < TB) {
+                    v4u wd[2];
+                    read_b(0, jb + 1, wd);
+                    unpack_b(wd, B[jb + 1]);
                 }
             }
-            if (b > 0) update(b - 1);
-            if (b > 0 && b < NB) {
-                // one MFMA, then the VALU share of the previous block's
-                // updates, four times
+            v16i (&p)[UPS] = acc[slot];
+            if constexpr (UNIT == 128) {
+                p[0] = mfma32(Acur[0], B[jb][0], zero);
+                p[0] = mfma32(Acur[1], B[jb][1], p[0]);
+                p[0] = mfma32(Acur[2], B[jb][2], p[0]);
+                p[0] = mfma32(Acur[3], B[jb][3], p[0]);
+            } else {
+                static_assert(UNIT == 64, "per-token mode has unit = group in {64, 128}");
+                p[0] = mfma32(Acur[0], B[jb][0], zero);
+                p[UPS - 1] = mfma32(Acur[1], B[jb][1], zero);
+                p[0] = mfma32(Acur[2], B[jb][2], p[0]);
+                p[UPS - 1] = mfma32(Acur[3], B[jb][3], p[UPS - 1]);
+            }
+            const int ub = b > 0 ? (b - 1) / TB : TA - 1, uj = b > 0 ? (b - 1) % TB : TB - 1;
+            update(ub, uj, acc[slot ^ 1], b > 0 ? w[uj] : wlast);
+            // keep the updates in this block: without a use here the
+            // compiler sinks them past the barrier branch of the last block
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 8 * UPS, 0);
-                }
+            for (int r = 0; r < 16; ++r) asm volatile("" ::"v"(f[ub][uj][r]));
+            // the block's reads, then one MFMA and the VALU share of the
+            // previous block's updates, four times
+            ds_first(ds_reads(b));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8 * UPS, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        st = st == NST - 1 ? 0 : st + 1;
+        st = stn;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ast[c] += dn;
+        bst += dn;
+        sst += dn;
+    };
+    // after the last step, its last block's updates
+    constexpr int LAST0 = (NB - 1) & 1, LAST1 = (2 * NB - 1) & 1;
+    if constexpr (NB % 2 == 0) {
+        for (int kb = 0; kb < NT; ++kb) step(kb, std::integral_constant<int, 0>{});
+        update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+    } else {
+        // an odd block count flips the slot parity every step: two steps
+        // per iteration keep the slots compile-time
+        int kb = 0;
+        for (; kb + 1 < NT; kb += 2) {
+            step(kb, std::integral_constant<int, 0>{});
+            step(kb + 1, std::integral_constant<int, 1>{});
+        }
+        if (kb < NT) {
+            step(kb, std::integral_constant<int, 0>{});
+            update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+        } else {
+            update(TA - 1, TB - 1, acc[LAST1], w[TB - 1]);
+        }
     }
-
     // ---- output ----
     // Each wave stages SB token blocks at a time in its own LDS slab (the
     // ring is free once every wave is past its last step) and writes whole
@@ -397,15 +547,56 @@ static int launch_g3(GemmArgs &a, hipStream_t st) {
     const dim3 grid(a.n_tiles * a.t_tiles), block(S::NTH);
     auto k = gemm3_kernel<TA, TB, WMW, WNW, UNIT, NST, OCC>;
     const size_t lds = (size_t)S::template lds_bytes<NST>();
-    static bool attr = false;
-    if (!attr) {
+    // the attribute is per device
+    static bool attr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -6;
+    if (!attr[dev]) {
         if (hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return -6;
-        attr = true;
+        attr[dev] = true;
     }
     hipLaunchKernelGGL(k, grid, block, lds, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -6;
 }
+
+// Tile choice. Per SIMD the kernel is bound by the FP32 chain of its
+// blocks, so each candidate is scored by the rounds of work-groups it needs
+// over the CUs times the 32x32 blocks per K step its busiest SIMD carries
+// per round (waves on that SIMD x blocks per wave); the small tile pays ~10%
+// for its larger L2 traffic per MAC (measured):
+//   256 x 256, 8 waves (2 per SIMD, 8 blocks each), one work-group per CU;
+//   256 x 160 (G128) / 64 x 160 (G64), 10 waves (3 on the busiest SIMD),
+//     one work-group per CU: fits the grid when the 256-row tile leaves
+//     CUs idle;
+//   128 x 64, 4 waves of 2 blocks, three work-groups per CU.
+static int choose_tile(const GemmArgs &a, int *bm) {
+    const bool g128 = a.group == 128;
+    struct Cand { int sel, bm, bng, wgs, simd_blocks; double penalty; };
+    const Cand cands[3] = {
+        {0, 256, g128 ? 16 : 8, 1, g128 ? 16 : 8, 1.0},
+        {g128 ? 9 : 8, g128 ? 256 : 64, 10, 1, g128 ? 12 : 3, 1.0},
+        {g128 ? 3 : 4, 128, 4, 3, 6, 1.1},
+    };
+    const long long cus = device_cus();
+    double best = 0.0;
+    int sel = -1;
+    for (const Cand &c : cands) {
+        long long nt = 0;
+        for (int i = 0; i < a.count; ++i) nt += (a.w[i].M / 16 + c.bng - 1) / c.bng;
+        const long long tiles = nt * ((a.T + c.bm - 1) / c.bm);
+        const long long rounds = (tiles + cus * c.wgs - 1) / (cus * c.wgs);
+        const double cost = (double)rounds * c.simd_blocks * c.penalty;
+        if (sel < 0 || cost < best) {
+            best = cost;
+            sel = c.sel;
+            *bm = c.bm;
+        }
+    }
+    return sel;
+}
+
+static int launch_tile(GemmArgs &a, int sel, hipStream_t st);
 
 int launch_gemm3(GemmArgs &a, hipStream_t st) {
     // per-token activation scale, plain FP16 weight scales, one split per token
@@ -416,40 +607,15 @@ int launch_gemm3(GemmArgs &a, hipStream_t st) {
         for (int s = 0; s < a.seg_count; ++s)
             if (a.w[i].seg_split[s] != 1) return 1;
     }
-    // Tile choice. Per SIMD the kernel is bound by the FP32 chain of its
-    // blocks, so each candidate is scored by the rounds of work-groups it
-    // needs over the CUs times the 32x32 blocks per K step its busiest SIMD
-    // carries per round (waves on that SIMD x blocks per wave); the small
-    // tile pays ~10% for its larger L2 traffic per MAC (measured):
-    //   256 x 256, 8 waves (2 per SIMD, 8 blocks each), one work-group per CU;
-    //   256 x 160 (G128) / 64 x 160 (G64), 10 waves (3 on the busiest SIMD),
-    //     one work-group per CU: fits the grid when the 256-row tile leaves
-    //     CUs idle;
-    //   128 x 64, 4 waves of 2 blocks, three work-groups per CU.
     // the gemm3_tile option (0..9) picks one configuration (tests, tuning)
-    int sel = options().gemm3_tile;
-    if (sel < 0) {
-        const bool g128 = a.group == 128;
-        struct Cand { int sel, bm, bng, wgs, simd_blocks; double penalty; };
-        const Cand cands[3] = {
-            {0, 256, g128 ? 16 : 8, 1, g128 ? 16 : 8, 1.0},
-            {g128 ? 9 : 8, g128 ? 256 : 64, 10, 1, g128 ? 12 : 3, 1.0},
-            {g128 ? 3 : 4, 128, 4, 3, 6, 1.1},
-        };
-        const long long cus = device_cus();
-        double best = 0.0;
-        for (const Cand &c : cands) {
-            long long nt = 0;
-            for (int i = 0; i < a.count; ++i) nt += (a.w[i].M / 16 + c.bng - 1) / c.bng;
-            const long long tiles = nt * ((a.T + c.bm - 1) / c.bm);
-            const long long rounds = (tiles + cus * c.wgs - 1) / (cus * c.wgs);
-            const double cost = (double)rounds * c.simd_blocks * c.penalty;
-            if (sel < 0 || cost < best) {
-                best = cost;
-                sel = c.sel;
-            }
-        }
-    }
+    const int forced = options().gemm3_tile;
+    if (forced >= 0) return launch_tile(a, forced, st);
+    int bm = 0;
+    const int sel = choose_tile(a, &bm);
+    return launch_tile(a, sel, st);
+}
+
+static int launch_tile(GemmArgs &a, int sel, hipStream_t st) {
     if (a.group == 128) {
         switch (sel) {
         case 8: return launch_g3<4, 1, 2, 5, 128, 3, 3>(a, st);   // 256 x 160, 10 waves

@@ -393,11 +393,14 @@ static int launch_w4(W4a4Args &a, hipStream_t st) {
     const dim3 grid(a.n_tiles * a.t_tiles), block(S::NTH);
     auto k = w4a4_kernel<TA, TB, WMW, WNW, NST, OCC>;
     const size_t lds = (size_t)S::template lds_bytes<NST>();
-    static bool attr = false;
-    if (!attr) {
+    // the attribute is per device
+    static bool attr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -6;
+    if (!attr[dev]) {
         if (hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return -6;
-        attr = true;
+        attr[dev] = true;
     }
     hipLaunchKernelGGL(k, grid, block, lds, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -6;

@@ -451,6 +451,13 @@ def test_gemm3_shapes(rows, K, T, group, gemm3_tile):
     assert_parity(got, ref, "bf16 + residual", bf16=True)
 
 
+@pytest.mark.parametrize("rows,K,T,group", [
+    # the tile chooser's own pick on ragged token counts
+    ([1040, 2064], 640, 300, 128), ([4096], 512, 600, 128), ([1040], 1024, 1100, 64)])
+def test_gemm3_auto_tile(rows, K, T, group):
+    test_gemm3_shapes(rows, K, T, group, None)
+
+
 @pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
 def test_baseline_config_gemm_general(name, gemm_general):
     run_config(name)
