@@ -163,9 +163,10 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
         const int rg = min(rg0 + j, RG - 1);
         so = (((uint32_t)rg * G + u) * 16 + half * 8) * 2;
     };
-    // With three waves per SIMD the registers are short: the lane parts are
-    // recomputed at each issue instead of held across the K loop.
-    constexpr bool kLaneRecompute = OCC >= 3;
+    // With three waves per SIMD and more than one block per wave the
+    // registers are short: the lane parts are recomputed at each issue
+    // instead of held across the K loop.
+    constexpr bool kLaneRecompute = OCC >= 3 && TA * TB > 1;
     uint32_t a_lane0 = 0, b_lane0 = 0, soff0 = 0;
     if constexpr (!kLaneRecompute) lane_offsets(lane, a_lane0, b_lane0, soff0);
     // The descriptors are built at each issue from scalars (a few SALU
@@ -300,7 +301,8 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     // (ib, 0) and weight block jb + 1 at block (0, jb), one block ahead.
     constexpr int NB = TA * TB;
     v4i B[TB][4];
-    v4u raw[2];                        // TB = 1: the next step's packed tile
+    v4u raw[2];                        // TB = 1, NB > 1: the next step's packed tile
+    v4i Bnext[4];                      // NB = 1: the next step's unpacked tile
     float w[TB][UPS], wnext[TB][UPS], wlast[UPS];
     v4i Acur[4], Anext[4];
     // acc[slot][u]: the 64-K group u of a block (one group per block at
@@ -310,12 +312,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     v16i acc[2][UPS];
     const v16i zero = {};
     auto read_next_step = [&](int d) {
-        if constexpr (TB == 1) {
-            read_b(d, 0, raw);
-        } else {
+        if constexpr (TB > 1) {
             v4u wd[2];
             read_b(d, 0, wd);
             unpack_b(wd, B[0]);
+        } else if constexpr (NB == 1) {
+            v4u wd[2];
+            read_b(d, 0, wd);
+            unpack_b(wd, Bnext);
+        } else {
+            read_b(d, 0, raw);          // (no registers to unpack it ahead)
         }
         read_w(d, wnext);
         read_a(d, 0, Anext);
@@ -353,6 +359,15 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     arrive(0);
     if (NST - 1 < NT) issue(NST - 1, NST - 1);
     read_next_step(0);
+    // With one block per step every read is of the next step's stage, so the
+    // tracked offsets point there instead.
+    constexpr bool kTrackNext = TA * TB == 1;
+    if constexpr (kTrackNext) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ast[c] += STAGE;
+        bst += STAGE;
+        sst += STAGE;
+    }
     // (complete here: the wait pass would otherwise assume them pending at
     // the loop head and wait on every step's first MFMA)
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -392,13 +407,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
 #pragma unroll
                 for (int c = 0; c < 4; ++c) Acur[c] = Anext[c];
             }
-            if constexpr (TB == 1) {
+            if constexpr (TB == 1 && NB == 1) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) B[0][c] = Bnext[c];
+            } else if constexpr (TB == 1) {
                 if (b == 0) unpack_b(raw, B[0]);
             }
             if (b == NB - 1) {
                 // the next step's first operands (after the last step: a
                 // harmless read of a stale stage)
-                read_next_step(dn);
+                read_next_step(kTrackNext ? 0 : dn);
             } else {
                 if (jb == 0 && ib + 1 < TA) read_a(0, ib + 1, Anext);
                 if (ib == 0 && jb + 1 < TB) {
@@ -436,11 +454,12 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        const int adv = kTrackNext ? ((stn == NST - 1 ? 0 : stn + 1) - stn) * STAGE : dn;
         st = stn;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) ast[c] += dn;
-        bst += dn;
-        sst += dn;
+        for (int c = 0; c < 4; ++c) ast[c] += adv;
+        bst += adv;
+        sst += adv;
     };
     // after the last step, its last block's updates
     constexpr int LAST0 = (NB - 1) & 1, LAST1 = (2 * NB - 1) & 1;
