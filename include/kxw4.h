@@ -215,7 +215,11 @@ int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4,
  * arithmetic (kernels_dpas.cpp:771-844, the same chain with zero point 0) for
  * T in [1, 16]. A K16 weight (group 16) runs x_gemv_w4a8_core_k16
  * (683-760): block-32 activations, two K16 half partials per K32 tile, one
- * serial accumulator per split, splits on K32 tiles; T in [1, 16]. */
+ * serial accumulator per split, splits on K32 tiles; T in [1, 16]. W8 and
+ * K16 stage every token's activation row in one work-group's LDS: where T
+ * rows do not fit (long K: at K = 17408 from T = 7 for W8, from 2-4 tokens
+ * for K16 depending on M) the tokens run in chunks that do, each streaming
+ * the weights again (same bits, more weight traffic). */
 int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
               const float *residual, int splits, void *stream);
 

@@ -514,10 +514,36 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // the per-unit activation scales and, for FP16|zp W4 weights, the
     // zero-point code sums, the split partials, the zero words
     const bool zp_table = wf == kWfW4 && a.scale_enc == 1;
-    size_t lds = (size_t)a.T * (a.K + 16) + (wf == kWfW8 ? 0 : (size_t)grmax * g * 32) +
-                 (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) +
-                 (S > 1 ? (size_t)spw * (S - 1) * 256 * 4 : 0) + 64;
-    if (lds > kRwLdsMax) return 1;
+    auto lds_for = [&](int T) {
+        return (size_t)T * (a.K + 16) + (wf == kWfW8 ? 0 : (size_t)grmax * g * 32) +
+               (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) +
+               (S > 1 ? (size_t)spw * (S - 1) * 256 * 4 : 0) + 64;
+    };
+    size_t lds = lds_for(a.T);
+    if (lds > kRwLdsMax) {
+        // The tokens' activations do not fit (long K at W8 or K16, which
+        // have no other kernel): run the tokens in chunks that do. A token's
+        // outputs depend on its own activation row only, so the bits are the
+        // same; every chunk streams the weights again.
+        int tc = a.T - 1;
+        while (tc > 0 && lds_for(tc) > kRwLdsMax) --tc;
+        if (tc == 0 || a.seg_count != 1 || a.dbg) return 1;
+        const size_t per_tok = a.block ? (size_t)(a.K / a.block) : 1;   // activation scales (and sums) per token
+        for (int t0 = 0; t0 < a.T; t0 += tc) {
+            DecodeArgs c = a;
+            c.T = std::min(tc, a.T - t0);
+            c.seg_end[0] = c.T;
+            c.q = a.q + (size_t)t0 * a.K;
+            c.ascale = a.ascale + (size_t)t0 * per_tok;
+            c.asum = a.asum ? a.asum + (size_t)t0 * per_tok : nullptr;
+            c.residual = a.residual ? a.residual + (size_t)t0 * a.w[0].M : nullptr;
+            for (int i = 0; i < a.count; ++i)
+                c.w[i].y = static_cast<uint8_t *>(a.w[i].y) + (size_t)t0 * a.w[i].M * (a.y_bf16 ? 2 : 4);
+            const int r = launch_rowwave(c, st);
+            if (r) return r < 0 ? r : -6;   // (a later chunk cannot be refused: it is no larger)
+        }
+        return 0;
+    }
     // no CU takes a (k+1)-th work-group of this launch at a time
     lds = std::max(lds, kRwLdsMax / (k + 1) + 1024);
     const dim3 block(64 * spw * wrg);

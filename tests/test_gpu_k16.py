@@ -72,6 +72,27 @@ def test_k16_gemv(M, K, T, splits):
     assert_parity(yr, O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, S, residual=res), "k16 + res")
 
 
+@pytest.mark.parametrize("M,T", [(1040, 8), (1040, 16), (5120, 16)])
+def test_k16_gemv_long_k(M, T):
+    # K = 17408 (the down projection): T tokens' activations do not fit in one
+    # work-group's LDS with the scale tables, so the launcher runs the tokens
+    # in chunks that do; the last chunk is shorter
+    K = 17408
+    print(f"k16 gemv long K M={M} K={K} T={T}", flush=True)
+    rng = np.random.default_rng(620 + T + M)
+    codes, scales, w = k16_weight(rng, M, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, M)).astype(np.float32)
+    a = ops.quantize_act(dev(x), 32)
+    q, s, sm = O.quantize_act(x, 32)
+    S = O.gemv_splits(M // 16)
+    y = ops.gemv(w, a, residual=dev(res)).cpu().numpy()
+    ref = O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, S, residual=res, rows=(0, 272))
+    assert_parity(y[:, :272], ref[:, :272], f"k16 long K T={T}")
+    ref2 = O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, S, residual=res, rows=(M - 144, M))
+    assert_parity(y[:, M - 144:], ref2[:, M - 144:], f"k16 long K T={T} last rows")
+
+
 @pytest.mark.parametrize("case", ["splits_on_k32_tiles", "single_accumulator"])
 def test_k16_order_cases(case):
     # the oracle's hand-derived order cases (tests/test_oracle.py) on the GPU

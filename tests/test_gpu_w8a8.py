@@ -95,6 +95,25 @@ def test_w8a8_gemv(M, K, T, splits):
     assert_parity(y, ref, f"gemv {M}x{K} T={T} S={S}")
 
 
+@pytest.mark.parametrize("T", [8, 16])
+def test_w8a8_gemv_long_k(T):
+    # K = 17408 (the down projection): at T >= 7 the activations do not fit
+    # in one work-group's LDS, so the launcher runs the tokens in chunks
+    M, K = 1040, 17408
+    print(f"w8a8 gemv long K M={M} K={K} T={T}", flush=True)
+    rng = np.random.default_rng(630 + T)
+    codes, scales, w = w8_weight(rng, M, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, M)).astype(np.float32)
+    a = ops.quantize_act(dev(x), 32)
+    q, s, sm = O.quantize_act(x, 32)
+    S = O.gemv_splits(M // 16)
+    y = ops.gemv(w, a, residual=dev(res)).cpu().numpy()
+    for rb, re in ((0, 272), (M - 144, M)):
+        ref = O.project(codes, scales, 32, O.SCALE_S8, q, s, sm, 32, O.VAR_GEMV, S, residual=res, rows=(rb, re))
+        assert_parity(y[:, rb:re], ref[:, rb:re], f"w8 long K T={T} rows {rb}:{re}")
+
+
 @pytest.mark.parametrize("M,K,T", [(512, 1024, 8), (256, 2048, 16), (512, 1024, 40), (1040, 640, 300)])
 def test_w8a8_gemm(M, K, T):
     # x_gemm_w8a8: one serial chain per output (forced split 1); T <= 16 runs
