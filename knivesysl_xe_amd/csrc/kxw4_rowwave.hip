@@ -71,6 +71,15 @@ template <int TT, int UNIT, int MODE, bool ALT2, int PF, int WF>
 __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(const DecodeArgs a) {
     constexpr int UPS = kTileK / UNIT;
     constexpr bool W8 = WF == kWfW8, K16 = WF == kWfK16;
+    // per-token W4 at group 64 (plain FP16 scales, unit = group): the tile's
+    // two scales ride in the ring too, one 2-byte load per lane and unit, so
+    // staging holds only the activations and the stream starts without
+    // waiting for the scale table's HBM reads (cfg2 M=1, 8.7 KB per
+    // row-group: 0.1-0.9 us faster on the boxes measured). At group 128 the
+    // table is a fifth of that and the extra load per tile cost more than the
+    // wait (cfg1: 0.7 us slower); group 32 would need four loads per tile
+    // and spills.
+    constexpr bool SRW4 = WF == kWfW4 && MODE == 0 && UNIT == 64;
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
@@ -121,8 +130,9 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // has no zero points and K16 folds them into the weight bytes), so the
     // other formats ask for less LDS
     const bool zp = WF == kWfW4 && a.scale_enc == 1;
-    // W8 scales are not staged: they stream through the ring (below)
-    float *Asc = reinterpret_cast<float *>(Sc + (W8 ? 0 : a.rw_grmax * G * 16));
+    // W8 and per-token W4 scales are not staged: they stream through the
+    // ring (below)
+    float *Asc = reinterpret_cast<float *>(Sc + (W8 || SRW4 ? 0 : a.rw_grmax * G * 16));
     int *Zs = reinterpret_cast<int *>(Asc + (MODE != 0 ? Nu * 16 : 0));
     float *Part = reinterpret_cast<float *>(Zs + (MODE != 0 && zp ? Nu * 16 : 0));
     // 16 zero words: the scale (and activation scale) read of a padded
@@ -136,7 +146,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // scales, each [G][16].
     const int kc = K / 16;
     const int act_chunks = T * (kc + 1);
-    const int total = act_chunks + (W8 ? 0 : n_gr * G * 2);
+    const int total = act_chunks + (W8 || SRW4 ? 0 : n_gr * G * 2);
     for (int c0 = wave * 64; c0 < total; c0 += nthreads) {
         const int x = c0 + lane;
         if (x < total) {
@@ -184,6 +194,9 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // holds unit j's scale of row n (the tile's 128 bytes of the [rg][G][16]
     // table); the chain spreads them to the row's lanes with shuffles
     uint32_t sring[W8 ? PF : 1];
+    // per-token W4: unit j of the tile's scale of this lane's row
+    uint16_t wring[SRW4 ? PF : 1][SRW4 ? UPS : 1];
+    const uint16_t *wsr = a.w[wsel].scales + (size_t)lrg * G * 16 + (row & 15);
     // tile i of the current split; an empty split (more splits than units)
     // or an idle wave reads a valid tile it never uses
     auto load = [&](int i, int p) {
@@ -192,8 +205,12 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
 #pragma unroll
         for (int h = 0; h < TB; ++h) ring[p][h] = __builtin_nontemporal_load(&wrow[t + 64 * h]);
         if constexpr (W8) sring[p] = wsc[(size_t)kt * (kTileK / 32) * 16];
+        if constexpr (SRW4) {
+#pragma unroll
+            for (int j = 0; j < UPS; ++j) wring[p][j] = wsr[((size_t)kt * UPS + j) * 16];
+        }
     };
-    constexpr int LPT = TB + (W8 ? 1 : 0);         // loads per tile
+    constexpr int LPT = TB + (W8 ? 1 : 0) + (SRW4 ? UPS : 0);   // loads per tile
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), p);
@@ -343,6 +360,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                             const uint16_t *sp = &sw[(MODE == 0 ? u : (u >> gsh)) * 16];
                             uint32_t sv;
                             if constexpr (W8) sv = in ? s8[j] : 0u;
+                            else if constexpr (SRW4) sv = in ? (uint32_t)wring[p][j] : 0u;
                             else sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
                             // GEMV: units at odd offsets from the split start feed the
                             // second accumulator. With an even ring and an even number
@@ -515,7 +533,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // zero-point code sums, the split partials, the zero words
     const bool zp_table = wf == kWfW4 && a.scale_enc == 1;
     auto lds_for = [&](int T) {
-        return (size_t)T * (a.K + 16) + (wf == kWfW8 ? 0 : (size_t)grmax * g * 32) +
+        return (size_t)T * (a.K + 16) + (wf == kWfW8 || (wf == kWfW4 && mode == 0 && unit == 64) ? 0 : (size_t)grmax * g * 32) +
                (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) +
                (S > 1 ? (size_t)spw * (S - 1) * 256 * 4 : 0) + 64;
     };
