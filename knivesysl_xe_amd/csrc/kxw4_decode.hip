@@ -91,6 +91,20 @@ __global__ __launch_bounds__(kDcThreads) void decode_kernel(const DecodeArgs a) 
     for (int c = 0; c < kScaleChunks; ++c)
         sreg[c] = sglob[min((int)threadIdx.x + kDcThreads * c, 2 * G - 1)];
 
+    // The output phase's per-token scale and residual of this thread's (at
+    // most two) outputs, loaded now: read after the split sum they add a
+    // dependent memory round trip at the end of the launch.
+    float tsc_pre[2] = {1.0f, 1.0f}, rsd_pre[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int o = (int)threadIdx.x + kDcThreads * k;
+        if (o < TL * 16) {
+            const int t = t0 + (o >> 4);
+            if (a.block == 0) tsc_pre[k] = a.ascale[t];
+            if (a.residual) rsd_pre[k] = a.residual[(size_t)t * M + rg * 16 + (o & 15)];
+        }
+    }
+
     const uint8_t *wbase = W.codes + (size_t)rg * NT * kTileBytes + lane * 16;
     // Activation rows. MFMA rows are independent: a row past the slice reads
     // a valid token and is never stored, so no lane predicate on the loads.
@@ -269,7 +283,11 @@ __global__ __launch_bounds__(kDcThreads) void decode_kernel(const DecodeArgs a) 
     if (DEBUG) return;
 
     // ---- phase 3: ordered split sum and output, one lane per output ----
-    for (int o = threadIdx.x; o < TL * 16; o += kDcThreads) {
+    static_assert(kDcThreads * 2 >= 64 * 16, "at most two outputs per thread (T <= 64)");
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int o = (int)threadIdx.x + kDcThreads * k;
+        if (o >= TL * 16) break;
         const int tl = o >> 4, nn = o & 15;
         const int Sp = split_of(tl);
         float val;
@@ -280,9 +298,9 @@ __global__ __launch_bounds__(kDcThreads) void decode_kernel(const DecodeArgs a) 
             for (int s = 0; s < Sp; ++s) val = val + Part[(s * TL + tl) * 16 + nn];
         }
         const int t = t0 + tl, row = rg * 16 + nn;
-        const float v = a.block == 0 ? val * (a.ascale[t] * 0.0625f) : val * 0.0625f;
+        const float v = a.block == 0 ? val * (tsc_pre[k] * 0.0625f) : val * 0.0625f;
         float out;
-        if (a.residual) out = v + a.residual[(size_t)t * M + row];
+        if (a.residual) out = v + rsd_pre[k];
         else if (alt2 && Sp > 1) out = v + 0.0f;
         else out = v;
         if (a.y_bf16) static_cast<uint16_t *>(W.y)[(size_t)t * M + row] = float_to_bf16(out);
