@@ -469,8 +469,11 @@ def read_traffic(name, sources):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # (a 20 us launch: 1000 warmup launches are ~20 ms, long enough for the
+    # shader clock to settle before the timed region; with 20 the timed
+    # region started during the ramp and read up to 8% slow)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--configs", default="cfg0,cfg2_m1,cfg2_m512,cfg3,cfg4",
                     help="extra BASELINE configs to report ('' for none)")
     ap.add_argument("--w4a4", default="cfg2_m512",
