@@ -407,6 +407,15 @@ def machine_probes(head_bytes):
         secs = timed(lambda _i: res.update(zip(("n", "ops"), ops.probe_mfma_i8(shape, iters, sink))), 3)
         out[f"{name}_TOPS"] = res["ops"] / secs / 1e12
         out[f"{name}_check"] = bool((sink[:res["n"]] == iters * k).all().item())
+    # issue mix of the GEMM's inner work: ns per block per SIMD for MFMA only,
+    # the FP32 chain only, both in one wave, both in separate waves
+    fsink = torch.empty(ops.PROBE_SINK_WORDS, dtype=torch.float32, device="cuda")
+    names = ("mfma", "chain", "mfma_chain_same_wave", "mfma_chain_split_waves")
+    for mode, wps in ((0, 1), (0, 2), (1, 2), (1, 4), (2, 1), (2, 2), (2, 4), (3, 2), (3, 4)):
+        ops.probe_issue(mode, wps, 10, fsink)
+        res = {}
+        secs = timed(lambda _i: res.update(blocks=ops.probe_issue(mode, wps, 4000, fsink)[1]), 3)
+        out[f"issue_{names[mode]}_w{wps}_ns_per_block"] = secs / res["blocks"] * 1e9
     buf = torch.empty(2 << 30, dtype=torch.uint8, device="cuda").fill_(1)
     n = (head_bytes + 4095) // 4096 * 4096
     slices = [buf[i * n:(i + 1) * n] for i in range(buf.numel() // n)]
@@ -421,6 +430,8 @@ def machine_probes(head_bytes):
         best_head = max(best_head, (n * 2 * len(slices) / secs / 1e9, shape))
     out["hbm_read_2GiB_GBps"], out["hbm_read_2GiB_shape"] = best_full
     out["hbm_read_headline_bytes_GBps"], out["hbm_read_headline_bytes_shape"] = best_head
+    out["issue_sample"] = ("kxw4_probe_issue, one work-group per CU, 4000 iterations of 4 blocks per wave; "
+                           "a block is 4 dependent v_mfma_i32_32x32x32_i8 and/or 16 cvt + 16 fma per lane")
     out["read_sample"] = (f"fastest of {ops.probe_read_shapes()} launch shapes; 2 GiB: 5 sweeps; headline "
                           f"bytes: {len(slices)} slices of {n} bytes rotated through 2 GiB, graph replay of "
                           f"{2 * len(slices)} launches as for the headline")
@@ -526,7 +537,8 @@ def main():
         log(f"probes: MFMA i8 32x32x32 {probes['mfma_i8_32x32x32_TOPS']:.0f} TOPS "
             f"(check {probes['mfma_i8_32x32x32_check']}), 16x16x64 {probes['mfma_i8_16x16x64_TOPS']:.0f} TOPS "
             f"(check {probes['mfma_i8_16x16x64_check']}); read {probes['hbm_read_2GiB_GBps']:.0f} GB/s (2 GiB), "
-            f"{probes['hbm_read_headline_bytes_GBps']:.0f} GB/s (headline bytes)")
+            f"{probes['hbm_read_headline_bytes_GBps']:.0f} GB/s (headline bytes); ns per block per SIMD: "
+            + ", ".join(f"{k[6:-13]} {v:.1f}" for k, v in probes.items() if k.startswith("issue_") and k.endswith("_ns_per_block")))
     if args.copy_mib:
         calibration_copy(args.copy_mib)
     log("cpu baseline (oracle on host cores)")

@@ -321,6 +321,19 @@ int kxw4_probe_mfma_i8(int shape, int iters, int32_t *sink, int sink_words, doub
 int kxw4_probe_read(const void *buf, size_t bytes, int shape, uint32_t *sink, int sink_words,
                     void *stream);
 int kxw4_probe_read_shapes(void);
+/* kxw4_probe_issue: the per-token GEMM's inner work without memory, one
+ * work-group of 4 * waves_per_simd waves (1-4 per SIMD) per CU. A block is
+ * four dependent v_mfma_i32_32x32x32_i8 (a 128-K step of a 32x32 output
+ * block) and/or its FP32 chain (16 int-to-float conversions and 16 FMAs per
+ * lane). mode 0: MFMAs only; 1: chain only; 2: both in one wave, block b's
+ * MFMAs interleaved with block b-1's chain; 3: MFMA waves and chain waves
+ * side by side on each SIMD (waves_per_simd even). *blocks receives the
+ * blocks each SIMD runs. One float per wave (deterministic; 0 for mode 1).
+ * No counterpart in the reference's probe: it separates the MFMA and VALU
+ * issue ceilings that bound the GEMM. Returns the words written, or -1 / -2 /
+ * -6. */
+int kxw4_probe_issue(int mode, int waves_per_simd, int iters, float *sink, int sink_words,
+                     double *blocks, void *stream);
 
 /* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
  * else group), from the same unpack and MFMA code as the projections. */

@@ -72,6 +72,7 @@ SIGNATURES = {
     "kxw4_probe_mfma_i8": (I, [I, I, P, I, C.POINTER(C.c_double), P]),
     "kxw4_probe_read": (I, [P, C.c_size_t, I, P, I, P]),
     "kxw4_probe_read_shapes": (I, []),
+    "kxw4_probe_issue": (I, [I, I, I, P, I, C.POINTER(C.c_double), P]),
     "kxw4_partials": (I, [WP, AP, P, P]),
 }
 

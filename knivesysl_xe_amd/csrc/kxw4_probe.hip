@@ -13,6 +13,14 @@
 // one of a few launch shapes; the caller times each shape and keeps the
 // fastest (the grid-stride pattern measured fastest for a pure stream on
 // this GPU).
+//
+// Issue mix: the per-token GEMM's inner work without memory. A "block" is
+// four dependent v_mfma_i32_32x32x32_i8 (one 128-K step of a 32x32 output
+// block) and/or its FP32 chain (16 int->float conversions and 16 FMAs per
+// lane). Mode 0 runs only the MFMAs, 1 only the chain, 2 both in one wave as
+// the GEMM interleaves them (block b's MFMAs with block b-1's chain), 3 both
+// in different waves of a SIMD; timed and counted per mode and waves per
+// SIMD, it gives what one SIMD can issue of each.
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 #include "../../include/kxw4.h"
@@ -84,6 +92,67 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const v4u *p, size_t n
     if ((threadIdx.x & 63) == 0) sink[((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
 }
 
+template <int MODE>
+__global__ __launch_bounds__(1024) void probe_issue_kernel(int iters, float w, float *sink) {
+    constexpr int NB = 4;                                  // blocks per iteration
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    v4i a = {lane, lane + 1, lane + 2, lane + 3}, b = {3, 5, 7, 9};
+    v16i acc[2] = {};
+    float f[NB][16];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) f[j][r] = 0.0f;
+    // mode 3: waves 0-3 of each group of eight (one per SIMD) run the MFMAs,
+    // waves 4-7 the chain
+    const bool mfma_role = MODE == 0 || MODE == 2 || (MODE == 3 && ((wave >> 2) & 1) == 0);
+    const bool valu_role = MODE == 1 || MODE == 2 || (MODE == 3 && ((wave >> 2) & 1) == 1);
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j <= NB; ++j) {
+            if (j < NB && mfma_role) {
+                v16i &p = acc[j & 1];
+                const v16i z = {};
+                // (opaque operands, so the MFMAs are not hoisted)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(a[e]));
+                p = mfma32(a, b, MODE == 2 ? z : p);
+                p = mfma32(b, a, p);
+                p = mfma32(a, b, p);
+                p = mfma32(b, a, p);
+            }
+            if (j > 0 && valu_role) {
+                v16i &p = acc[(j - 1) & 1];
+                if (MODE != 2) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(p[r]));
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) f[j - 1][r] = __builtin_fmaf((float)p[r], w, f[j - 1][r]);
+            }
+            if (MODE == 2 && j > 0 && j < NB) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += f[j][r];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += (float)acc[0][r] + (float)acc[1][r];
+    // one word per wave, summed in a fixed order (the same every run)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) sink[blockIdx.x * (blockDim.x >> 6) + wave] = s;
+}
+
 // launch shapes of the read probe: (work-groups per CU, threads, ring depth)
 struct ReadShape { int per_cu, threads, ring; };
 constexpr ReadShape kReadShapes[] = {
@@ -133,3 +202,24 @@ extern "C" int kxw4_probe_read(const void *buf, size_t bytes, int shape, uint32_
 }
 
 extern "C" int kxw4_probe_read_shapes(void) { return kReadShapeCount; }
+
+extern "C" int kxw4_probe_issue(int mode, int waves_per_simd, int iters, float *sink, int sink_words,
+                                double *blocks, void *stream) {
+    if (mode < 0 || mode > 3 || waves_per_simd < 1 || waves_per_simd > 4 || iters < 1 || !sink) return KXW4_EARG;
+    // split roles need a wave of each role on every SIMD
+    if (mode == 3 && waves_per_simd % 2) return KXW4_EARG;
+    const int groups = device_cus(), threads = 256 * waves_per_simd;
+    if (sink_words < groups * 4 * waves_per_simd) return KXW4_ESHAPE;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const float w = 1.0001f;
+    switch (mode) {
+    case 0: hipLaunchKernelGGL(probe_issue_kernel<0>, dim3(groups), dim3(threads), 0, st, iters, w, sink); break;
+    case 1: hipLaunchKernelGGL(probe_issue_kernel<1>, dim3(groups), dim3(threads), 0, st, iters, w, sink); break;
+    case 2: hipLaunchKernelGGL(probe_issue_kernel<2>, dim3(groups), dim3(threads), 0, st, iters, w, sink); break;
+    default: hipLaunchKernelGGL(probe_issue_kernel<3>, dim3(groups), dim3(threads), 0, st, iters, w, sink); break;
+    }
+    if (hipGetLastError() != hipSuccess) return KXW4_EHIP;
+    // blocks per SIMD: 4 per iteration and wave (split roles: per role pair)
+    if (blocks) *blocks = 4.0 * iters * (mode == 3 ? waves_per_simd / 2 : waves_per_simd);
+    return groups * 4 * waves_per_simd;
+}

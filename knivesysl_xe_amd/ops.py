@@ -538,6 +538,19 @@ def probe_mfma_i8(shape: int, iters: int, sink: torch.Tensor) -> tuple:
     return n, ops_count.value
 
 
+def probe_issue(mode: int, waves_per_simd: int, iters: int, sink: torch.Tensor) -> tuple:
+    """Enqueue the issue-mix probe (mode 0 MFMA only, 1 FP32 chain only, 2 both
+    in one wave, 3 both in separate waves) on the current stream; `sink` is
+    float32. Returns (sink words written, blocks per SIMD)."""
+    if sink.dtype != torch.float32:
+        raise _lib.KxError("kxw4_probe_issue", _lib.EARG)
+    blocks = C.c_double()
+    n = lib().kxw4_probe_issue(mode, waves_per_simd, iters, _ptr(sink), sink.numel(), C.byref(blocks), _stream())
+    if n < 0:
+        raise _lib.KxError("kxw4_probe_issue", n)
+    return n, blocks.value
+
+
 def probe_read_shapes() -> int:
     return lib().kxw4_probe_read_shapes()
 

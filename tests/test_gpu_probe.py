@@ -1,7 +1,8 @@
-"""The machine probes (kxw4_probe_mfma_i8, kxw4_probe_read; counterpart of
+"""The machine probes (kxw4_probe_mfma_i8, kxw4_probe_read, kxw4_probe_issue; counterpart of
 xpu/probe/dpas_probe.cpp): the all-ones MFMA chains must end at exactly
-iters * K in every wave (the reference's `d == iters * K` check), and the read
-probe must cover the buffer and reject bad arguments.
+iters * K in every wave (the reference's `d == iters * K` check), the read
+probe must cover the buffer, the issue probe must write one deterministic word
+per wave, and all of them must reject bad arguments.
 """
 import pytest
 
@@ -57,3 +58,40 @@ def test_read_probe(shape):
         ops.probe_mfma_i8(2, 10, sink)               # no such shape
     with pytest.raises(KxError):
         ops.probe_mfma_i8(0, 10, sink[:16])          # sink too small
+
+
+@pytest.mark.parametrize("mode,wps", [(0, 1), (1, 3), (2, 2), (3, 4)])
+def test_issue_probe(mode, wps):
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.full((ops.PROBE_SINK_WORDS,), 7.0, dtype=torch.float32, device="cuda")
+    n, blocks = ops.probe_issue(mode, wps, 25, sink)
+    first = sink[:n].clone()
+    torch.cuda.synchronize()
+    assert n == cus * 4 * wps                        # one word per wave
+    assert blocks == 4 * 25 * (wps // 2 if mode == 3 else wps)
+    assert torch.all(sink[n:] == 7.0)
+    assert torch.isfinite(first).all()
+    wave = torch.arange(n, device="cuda") % (4 * wps)
+    if mode == 1:
+        assert torch.all(first == 0.0)               # the chain alone folds zeros
+    elif mode == 3:                                  # waves 4-7 of each eight run the chain alone
+        chain = (wave >> 2) & 1 == 1
+        assert torch.all(first[chain] == 0.0) and torch.all(first[~chain] != 0.0)
+    else:
+        assert torch.all(first != 0.0)
+        assert torch.all(first == first[0])          # every wave runs the same work
+    # and the same words run after run
+    ops.probe_issue(mode, wps, 25, sink)
+    torch.cuda.synchronize()
+    assert torch.equal(sink[:n], first)
+
+
+def test_issue_probe_arguments():
+    sink = torch.zeros(ops.PROBE_SINK_WORDS, dtype=torch.float32, device="cuda")
+    for mode, wps, iters in ((4, 1, 1), (-1, 1, 1), (0, 0, 1), (0, 5, 1), (3, 3, 1), (0, 1, 0)):
+        with pytest.raises(KxError):
+            ops.probe_issue(mode, wps, iters, sink)
+    with pytest.raises(KxError):
+        ops.probe_issue(0, 1, 1, sink[:16])          # sink too small
+    with pytest.raises(KxError):
+        ops.probe_issue(0, 1, 1, sink.view(torch.int32))  # float32 sink only
