@@ -80,6 +80,12 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // wait (cfg1: 0.7 us slower); group 32 would need four loads per tile
     // and spills.
     constexpr bool SRW4 = WF == kWfW4 && MODE == 0 && UNIT == 64;
+    // TT = 1 or 2 (per-token W4, at most TT tokens): the MFMA leaves token
+    // 4*(l/16) + r in register r of lane l, so only registers r < TT hold
+    // real tokens and the chain runs on those alone (T = 1: a quarter of the
+    // conversions and FMAs)
+    constexpr int NR = TT < 4 ? TT : 4;
+    static_assert(TT >= 8 || (WF == kWfW4 && MODE == 0), "short-token chains: per-token W4");
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     const bool gemm_var = a.variant == kVarGemm;
     // this lane's activation row (MFMA row n; with up to 8 tokens rows 8-15
     // repeat rows 0-7 and are never stored) and its K-slot group
-    const int ta = TT == 8 ? min(n & 7, T - 1) : min(n, T - 1);
+    const int ta = TT <= 8 ? min(n & 7, T - 1) : min(n, T - 1);
     const int8_t *abase = Act + (size_t)ta * pitch + 16 * g4;
     float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -371,7 +377,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                             if constexpr (MODE == 0) {
                                 const float ws = half_bits_to_float((uint16_t)sv);
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) F[r] = __builtin_fmaf((float)acc[r], ws, F[r]);
+                                for (int r = 0; r < NR; ++r) F[r] = __builtin_fmaf((float)acc[r], ws, F[r]);
                             } else {
                                 const float ws = half_bits_to_float(zp ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
                                 const int z = sext4(sv);
@@ -460,7 +466,7 @@ static int rw_launch(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hip
 
 template <int TT, int UNIT, int MODE, bool ALT2, int WF>
 static int rw_ring(const DecodeArgs &a, int pf, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-    if constexpr (WF != kWfK16) {
+    if constexpr (WF != kWfK16 && TT >= 8) {
         if (pf == 8) return rw_launch<TT, UNIT, MODE, ALT2, 8, WF>(a, grid, block, lds, st);
     }
     return rw_launch<TT, UNIT, MODE, ALT2, 4, WF>(a, grid, block, lds, st);
@@ -472,8 +478,12 @@ static int rw_mode(const DecodeArgs &a, int mode, int pf, dim3 grid, dim3 block,
     if (mode == 0)
         return alt2 ? rw_ring<TT, UNIT, 0, true, kWfW4>(a, pf, grid, block, lds, st)
                     : rw_ring<TT, UNIT, 0, false, kWfW4>(a, pf, grid, block, lds, st);
-    return alt2 ? rw_ring<TT, UNIT, 1, true, kWfW4>(a, pf, grid, block, lds, st)
-                : rw_ring<TT, UNIT, 1, false, kWfW4>(a, pf, grid, block, lds, st);
+    if constexpr (TT < 8) {
+        return 1;
+    } else {
+        return alt2 ? rw_ring<TT, UNIT, 1, true, kWfW4>(a, pf, grid, block, lds, st)
+                    : rw_ring<TT, UNIT, 1, false, kWfW4>(a, pf, grid, block, lds, st);
+    }
 }
 
 template <int TT>
@@ -577,6 +587,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     if (wf == kWfK16)
         return a.T <= 8 ? rw_ring<8, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st)
                         : rw_ring<16, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st);
+    // one or two tokens in per-token mode: the short chains (4-deep ring)
+    if (mode == 0 && pf == 4 && a.T == 1) return rw_unit<1>(a, unit, mode, pf, grid, block, lds, st);
+    if (mode == 0 && pf == 4 && a.T == 2) return rw_unit<2>(a, unit, mode, pf, grid, block, lds, st);
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf, grid, block, lds, st);
     return rw_unit<16>(a, unit, mode, pf, grid, block, lds, st);
 }

@@ -376,6 +376,11 @@ def test_cfg2_m1_rowwave_ring(ring):
     ([2048, 512], 4096, 2, 64, 32, 1, "gemm", 0),
     ([5120], 17408, 1, 64, 32, 1, "gemv", 0),
     ([1024], 2048, 8, 32, 32, 1, "fanout", 0),
+    # one or two tokens per token scale: the short-chain instances
+    ([4096, 1024], 5120, 1, 128, 0, 0, "fanout", 0),
+    ([2048], 4096, 2, 64, 0, 0, "gemv", 0),
+    ([512, 48], 1024, 1, 32, 0, 0, "gemm", 4),
+    ([1040], 17408, 2, 64, 0, 0, "gemm", 0),
 ])
 def test_decode_shapes(rows, K, T, group, block, enc, variant, forced):
     # decode shapes off the BASELINE grid: fewer row-groups than CUs, mixed
