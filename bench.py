@@ -74,8 +74,14 @@ def launcher(cfg, act, outs):
     return lambda w: ops.gemm_fanout(w, act, dt, offsets=cfg.offsets, outs=outs)
 
 
+WARM_MS = 20.0      # warm-up GPU time before a timed region (the shader clock's ramp)
+
+
 def time_graph(run, copies, steps, warmup):
-    """Capture `steps` launches in one graph, replay it between syncs."""
+    """Capture `steps` launches in one graph, replay it between syncs. With
+    warmup=None the warm-up graph holds about WARM_MS of launches, sized from
+    a replay of 10 (the clock ramps up over the first milliseconds of load, so
+    a fixed small count under-warms short kernels)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -92,6 +98,18 @@ def time_graph(run, copies, steps, warmup):
                 run(copies[(offset + i) % len(copies)])
         return g
 
+    if warmup is None:
+        g10 = capture(10, 0)
+        g10.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g10.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per_ms = max(e0.elapsed_time(e1) / 10, 1e-3)
+        warmup = int(min(max(WARM_MS / per_ms, 20), 20000))
+        del g10
     gw = capture(max(warmup, 1), 0)
     gt = capture(steps, max(warmup, 1))
     torch.cuda.synchronize()
@@ -491,7 +509,8 @@ def main():
                     help="K64 configs to also run through the W4A4 GEMM ('' for none)")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
     ap.add_argument("--no-probes", action="store_true", help="skip the MFMA / HBM read probes")
-    ap.add_argument("--extra-steps", type=int, default=50)
+    ap.add_argument("--extra-steps", type=int, default=200,
+                    help="timed launches per extra config (each after ~20 ms of warm-up launches)")
     ap.add_argument("--cpu-budget", type=float, default=3.0,
                     help="seconds of CPU-baseline timing per config")
     ap.add_argument("--eager", action="store_true",
@@ -516,19 +535,19 @@ def main():
     for name in [c for c in args.configs.split(",") if c]:
         cfg = workloads.CONFIGS[name]
         log(f"{name}: {cfg.note}")
-        extra[name] = measure(cfg, args.extra_steps, 5, args.eager)
+        extra[name] = measure(cfg, args.extra_steps, 5 if args.eager else None, args.eager)
         e = extra[name]
         log(f"{name}: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, {e['TOPS']:.1f} TOPS, "
             f"frac {e['roofline_frac']:.3f}, exact={e['bit_exact_vs_oracle_rows0_512']}")
     for name in [c for c in args.w4a4.split(",") if c]:
         cfg = workloads.CONFIGS[name]
         log(f"{name}_w4a4: W4A4 GEMM on the {name} shape (s4 activations, FP16|zp K64 weight)")
-        e = extra[f"{name}_w4a4"] = measure_w4a4(cfg, args.extra_steps, 5, args.eager)
+        e = extra[f"{name}_w4a4"] = measure_w4a4(cfg, args.extra_steps, 5 if args.eager else None, args.eager)
         log(f"{name}_w4a4: {e['kernel_us']:.2f} us, {e['TOPS']:.1f} TOPS, frac {e['roofline_frac']:.3f}, "
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     if not args.no_w8a8:
         log("lm_head_w8a8: W8A8 GEMM, spec wave T=8, K=5120, N=248320 int8")
-        e = extra["lm_head_w8a8"] = measure_w8a8(20, 3, args.eager)
+        e = extra["lm_head_w8a8"] = measure_w8a8(args.extra_steps, 3 if args.eager else None, args.eager)
         log(f"lm_head_w8a8: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, frac {e['roofline_frac']:.3f}, "
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     probes = None
