@@ -285,8 +285,13 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             // One ring of PF tiles starting at tile ib of the split. PRED
             // marks the rings that may hold padded positions or units outside
             // the split.
-            auto ring_pass = [&](int ib, auto pred) {
+            // LOADS: whether the pass refills each slot with the tile PF
+            // ahead. The split's last pass loads nothing: a load past the
+            // split's last tile would hold its registers, and every later use
+            // of them (the split sum, the epilogue) would wait for it.
+            auto ring_pass = [&](int ib, auto pred, auto loads) {
                 constexpr bool PRED = decltype(pred)::value;
+                constexpr bool LOADS = decltype(loads)::value;
                 const int8_t *ar = abase + (size_t)(kt0 + ib) * kTileK;
 #pragma unroll
                 for (int p = 0; p < PF; ++p) {
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                             }
                         }
                     }
-                    load(min(i + PF, ntw - 1), p);
+                    if constexpr (LOADS) load(min(i + PF, ntw - 1), p);
                     // keep each slot's unpack behind the previous slot's load, so
                     // the wait before it covers only that slot
                     __builtin_amdgcn_sched_barrier(0);
@@ -405,10 +410,24 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             // whole rings run unpredicated when the split starts and ends on
             // tile boundaries; the rest (at most one ring then) is predicated
             const bool aligned = u0 % UPS == 0 && u1 % UPS == 0;
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            // Only the per-token group-64 instances take the load-free last
+            // pass (cfg2 M=1: 13.3-13.9 against 13.7-14.3 us). The others keep
+            // one refilling pass: a second copy of their ring spills (K16,
+            // group 32), takes more than the 80 registers that let two 10-wave
+            // work-groups share a CU (group 128), or measured slower (W8:
+            // lm_head 249 against 242 us).
+            constexpr bool kLastNoLoads = WF == kWfW4 && UNIT == 64 && MODE == 0;
             int ib = 0;
+            // (the last ring, full or not, runs predicated: one copy of the
+            // ring code without loads, not two)
             if (aligned)
-                for (; ib + PF <= ntw; ib += PF) ring_pass(ib, std::false_type{});
-            for (; ib < ntw; ib += PF) ring_pass(ib, std::true_type{});
+                for (; ib + PF < ntw || (!kLastNoLoads && ib + PF <= ntw); ib += PF) ring_pass(ib, F_{}, T_{});
+            for (; ib < ntw; ib += PF) {
+                if (!kLastNoLoads || ib + PF < ntw) ring_pass(ib, T_{}, T_{});
+                else if constexpr (kLastNoLoads) ring_pass(ib, T_{}, F_{});
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float v = (ALT2 && !K16) ? f0[r] + f1[r] : f0[r];
@@ -433,7 +452,20 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
         return;
     }
     if (!act) return;
-    const DecodeWeight &W = a.w[wsel];
+    // this lane's output buffer and height, chosen with uniform indices
+    // (scalar loads of the kernel arguments, made opaque so the choice stays
+    // a select): a per-lane index into the kernel arguments is a vector
+    // memory load, whose wait would also wait for the ring's last loads
+    __attribute__((address_space(1))) uint8_t *wy = (__attribute__((address_space(1))) uint8_t *)a.w[0].y;
+    int wm = a.w[0].M;
+#pragma unroll
+    for (int i = 1; i < kMaxWeights; ++i) {
+        __attribute__((address_space(1))) uint8_t *yi = (__attribute__((address_space(1))) uint8_t *)a.w[i < a.count ? i : 0].y;
+        int mi = a.w[i < a.count ? i : 0].M;
+        asm volatile("" : "+s"(yi), "+s"(mi));
+        wy = wsel == i ? yi : wy;
+        wm = wsel == i ? mi : wm;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int t = 4 * g4 + r;
@@ -443,8 +475,8 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
         if (a.residual) out = v + rsd[r];
         else if (ALT2 && S > 1) out = v + 0.0f;
         else out = v;
-        if (a.y_bf16) static_cast<uint16_t *>(W.y)[(size_t)t * W.M + lrow] = float_to_bf16(out);
-        else static_cast<float *>(W.y)[(size_t)t * W.M + lrow] = out;
+        if (a.y_bf16) ((__attribute__((address_space(1))) uint16_t *)wy)[(size_t)t * wm + lrow] = float_to_bf16(out);
+        else ((__attribute__((address_space(1))) float *)wy)[(size_t)t * wm + lrow] = out;
     }
 }
 
