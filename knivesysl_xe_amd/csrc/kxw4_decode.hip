@@ -222,8 +222,14 @@ __global__ __launch_bounds__(kDcThreads) void decode_kernel(const DecodeArgs a) 
     }
     __syncthreads();
 
-    // split count of slice token tl (its packed segment's plan)
+    // split count of slice token tl (its packed segment's plan). With one
+    // segment it is a scalar, read once and made opaque: a per-lane segment
+    // index into the kernel arguments is a vector memory load, and its wait
+    // after the stream adds a memory round trip to the launch.
+    int split1 = W.seg_split[0];
+    asm volatile("" : "+s"(split1));
     auto split_of = [&](int tl) {
+        if (a.seg_count == 1) return split1;
         const int tg = t0 + tl;
         int seg = 0;
         while (seg + 1 < a.seg_count && tg >= a.seg_end[seg]) ++seg;
