@@ -353,12 +353,20 @@ template <int WM, int UNIT>
 static void launch_wm_unit(const GemmArgs &a, int mode, bool splits, bool debug, dim3 grid,
                            hipStream_t st) {
     const dim3 block(kGemmThreads);
-    if (debug) {
-        hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, true, false>), grid, block, 0, st, a);
-    } else if (splits) {
-        if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, true, false, false>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, false, false>), grid, block, 0, st, a);
-    } else {
+    // (split rows and debug runs always take the narrow tile: the wide one
+    // is built for the plain chain only)
+    if constexpr (WM == 2) {
+        if (debug) {
+            hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, true, false>), grid, block, 0, st, a);
+            return;
+        }
+        if (splits) {
+            if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, true, false, false>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, true, false, false>), grid, block, 0, st, a);
+            return;
+        }
+    }
+    {
         if (mode == 0) hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 0, false, false, false>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((gemm_kernel<WM, UNIT, 1, false, false, false>), grid, block, 0, st, a);
     }

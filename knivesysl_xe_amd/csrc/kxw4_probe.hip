@@ -92,10 +92,11 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const v4u *p, size_t n
     if ((threadIdx.x & 63) == 0) sink[((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
 }
 
-template <int MODE>
-__global__ __launch_bounds__(1024) void probe_issue_kernel(int iters, float w, float *sink) {
+// One wave's share of the issue probe in mode M (0: MFMAs, 1: the chain, 2:
+// both interleaved); returns the lane's sum of its accumulators.
+template <int M>
+__device__ __forceinline__ float issue_run(int iters, float w, int lane) {
     constexpr int NB = 4;                                  // blocks per iteration
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     v4i a = {lane, lane + 1, lane + 2, lane + 3}, b = {3, 5, 7, 9};
     v16i acc[2] = {};
     float f[NB][16];
@@ -103,34 +104,30 @@ __global__ __launch_bounds__(1024) void probe_issue_kernel(int iters, float w, f
     for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) f[j][r] = 0.0f;
-    // mode 3: waves 0-3 of each group of eight (one per SIMD) run the MFMAs,
-    // waves 4-7 the chain
-    const bool mfma_role = MODE == 0 || MODE == 2 || (MODE == 3 && ((wave >> 2) & 1) == 0);
-    const bool valu_role = MODE == 1 || MODE == 2 || (MODE == 3 && ((wave >> 2) & 1) == 1);
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int j = 0; j <= NB; ++j) {
-            if (j < NB && mfma_role) {
+            if (j < NB && M != 1) {
                 v16i &p = acc[j & 1];
                 const v16i z = {};
                 // (opaque operands, so the MFMAs are not hoisted)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(a[e]));
-                p = mfma32(a, b, MODE == 2 ? z : p);
+                p = mfma32(a, b, M == 2 ? z : p);
                 p = mfma32(b, a, p);
                 p = mfma32(a, b, p);
                 p = mfma32(b, a, p);
             }
-            if (j > 0 && valu_role) {
+            if (j > 0 && M != 0) {
                 v16i &p = acc[(j - 1) & 1];
-                if (MODE != 2) {
+                if (M != 2) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(p[r]));
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) f[j - 1][r] = __builtin_fmaf((float)p[r], w, f[j - 1][r]);
             }
-            if (MODE == 2 && j > 0 && j < NB) {
+            if (M == 2 && j > 0 && j < NB) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -147,6 +144,21 @@ __global__ __launch_bounds__(1024) void probe_issue_kernel(int iters, float w, f
         for (int r = 0; r < 16; ++r) s += f[j][r];
 #pragma unroll
     for (int r = 0; r < 16; ++r) s += (float)acc[0][r] + (float)acc[1][r];
+    return s;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(1024) void probe_issue_kernel(int iters, float w, float *sink) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float s;
+    if constexpr (MODE == 3) {
+        // waves 0-3 of each group of eight (one per SIMD) run the MFMAs,
+        // waves 4-7 the chain: two loops, so neither holds the other's
+        // registers
+        s = ((wave >> 2) & 1) == 0 ? issue_run<0>(iters, w, lane) : issue_run<1>(iters, w, lane);
+    } else {
+        s = issue_run<MODE>(iters, w, lane);
+    }
     // one word per wave, summed in a fixed order (the same every run)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
