@@ -429,7 +429,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                 else if constexpr (kLastNoLoads) ring_pass(ib, T_{}, F_{});
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < NR; ++r) {
                 const float v = (ALT2 && !K16) ? f0[r] + f1[r] : f0[r];
                 // split 0 stays in the registers of the wave that adds the splits
                 if (S > 1 && s > 0) Part[((sl * (S - 1) + s - 1) * 4 + r) * 64 + lane] = v;
@@ -442,11 +442,47 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     if (S > 1) {
         lds_sync();
         if (!active || wj != 0) return;
+        // S - 1 partials per live register, all read before the ordered
+        // adds (a loop over s would wait for each read in turn)
+        // (registers r in groups of RB, at most 16 reads in flight)
+        auto split_sum = [&](auto sc) {
+            constexpr int SC = decltype(sc)::value;
+            constexpr int RB = (SC - 1) * NR <= 16 ? NR : 1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float sum = 0.0f + res[r];
-            for (int s = 1; s < S; ++s) sum = sum + Part[((sl * (S - 1) + s - 1) * 4 + r) * 64 + lane];
-            res[r] = sum;
+            for (int r0 = 0; r0 < NR; r0 += RB) {
+                float p[RB][SC - 1];
+#pragma unroll
+                for (int r = 0; r < RB; ++r)
+#pragma unroll
+                    for (int j = 1; j < SC; ++j)
+                        p[r][j - 1] = Part[((sl * (SC - 1) + j - 1) * 4 + r0 + r) * 64 + lane];
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    float sum = 0.0f + res[r0 + r];
+#pragma unroll
+                    for (int j = 1; j < SC; ++j) sum = sum + p[r][j - 1];
+                    res[r0 + r] = sum;
+                }
+            }
+        };
+        // (S is a power of two, at most 16: checked by the launcher). Only
+        // the one- and two-token instances, whose few live registers make
+        // S - 1 the whole wait: in the others the batch costs registers
+        // that the two work-groups per CU of the group-128 launches need.
+        if constexpr (NR < 4) {
+            switch (S) {
+            case 2: split_sum(std::integral_constant<int, 2>{}); break;
+            case 4: split_sum(std::integral_constant<int, 4>{}); break;
+            case 8: split_sum(std::integral_constant<int, 8>{}); break;
+            default: split_sum(std::integral_constant<int, 16>{}); break;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float sum = 0.0f + res[r];
+                for (int s = 1; s < S; ++s) sum = sum + Part[((sl * (S - 1) + s - 1) * 4 + r) * 64 + lane];
+                res[r] = sum;
+            }
         }
     } else if (!active) {
         return;
