@@ -362,11 +362,16 @@ int launch_decode(DecodeArgs &a, bool debug, hipStream_t st) {
     // Per-token weights with at most 8 tokens and no more row-groups than
     // CUs stay here: one work-group per row-group whose waves read
     // consecutive kilobytes beats the row-wave kernel's per-split streams
-    // when every CU holds at most one row-group (cfg0: 6.9 -> 6.3 us).
+    // when every CU holds at most one row-group (T = 4: 5.5 against 6.4 us
+    // at M = K = 4096) -- except for one or two tokens with at most 8 splits
+    // of at most 8 tiles each, where the row-wave kernel's short chains and
+    // single ring win (cfg0: 5.3 against 5.4 us; K = 2048: 4.6 against 5.0).
     if (force != kDecodeRowwave && a.block == 0 && a.scale_enc == 0 && a.T <= 8) {
         int rgs = 0;
         for (int i = 0; i < a.count; ++i) rgs += a.w[i].M / 16;
-        if (rgs <= device_cus()) no_rowwave = true;
+        const int S = a.w[0].seg_split[0];
+        const bool short_rowwave = a.T <= 2 && S <= 8 && (a.K / kTileK) <= 8 * S;
+        if (rgs <= device_cus() && !short_rowwave) no_rowwave = true;
     }
     if (!debug && !no_rowwave) {
         const int r = launch_rowwave(a, st);
