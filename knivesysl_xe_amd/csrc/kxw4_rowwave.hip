@@ -476,6 +476,8 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             case 8: split_sum(std::integral_constant<int, 8>{}); break;
             default: split_sum(std::integral_constant<int, 16>{}); break;
             }
+        } else if (S == 2) {
+            split_sum(std::integral_constant<int, 2>{});
         } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
