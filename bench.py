@@ -181,7 +181,7 @@ def measure(cfg, steps, warmup, eager=False):
     # with few launches the replay's start-up dominates a few-us kernel)
     from knivesysl_xe_amd import ops
     qa = ops.QuantAct.empty(cfg.tokens, cfg.K, 0)
-    qsecs, _ = time_graph(lambda _c: ops.quantize_act(x, 0, out=qa), [None], QUANT_STEPS, 2)
+    qsecs, _ = time_graph(lambda _c: ops.quantize_act(x, 0, out=qa), [None], QUANT_STEPS, None)
     quant_us = qsecs / QUANT_STEPS * 1e6
     per = secs / steps
     res = {
@@ -235,7 +235,7 @@ def measure_w4a4(cfg, steps, warmup, eager=False):
         else got.cpu().numpy().view(np.uint32)
     exact = bool(np.array_equal(got, ref[:, :512].view(got.dtype)))
     qa = ops.QuantActS4.empty(cfg.tokens, cfg.K)
-    qsecs, _ = time_graph(lambda _c: ops.quantize_act_s4(x, out=qa), [None], QUANT_STEPS, 2)
+    qsecs, _ = time_graph(lambda _c: ops.quantize_act_s4(x, out=qa), [None], QUANT_STEPS, None)
     per = secs / steps
     N = sum(cfg.rows)
     res = {
