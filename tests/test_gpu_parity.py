@@ -591,3 +591,31 @@ def test_gemm_agrees_with_gemv_gate():
         for t in range(T):
             c = got[t] @ ref[t] / np.sqrt((got[t] @ got[t]) * (ref[t] @ ref[t]))
             assert c >= 0.9999, (T, t, c)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("S", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("variant", ["gemv", "gemm"])
+def test_rowwave_short_token_splits(T, S, variant):
+    # the one- and two-token row-wave instances (live-register chains, split
+    # partials read at once before the ordered sum) at every split count,
+    # both chain variants, with and without residual, against the oracle
+    print(f"short-token rowwave T={T} S={S} {variant}", flush=True)
+    M, K, group = 1040, 4096, 128
+    rng = np.random.default_rng(T * 100 + S)
+    codes, sc = rand_weight(rng, M, K, group, 0)
+    w = weight(codes, sc, group, 0)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, M)).astype(np.float32)
+    a = ops.quantize_act(dev(x), 0)
+    q, s, sm = O.quantize_act(x, 0)
+    var = O.VAR_GEMV if variant == "gemv" else O.VAR_GEMM
+    with ops.option("decode_kernel", 2):
+        for r in (None, res):
+            if variant == "gemv":
+                got = to_np(ops.gemv(w, a, residual=None if r is None else dev(r), splits=S))
+            else:
+                got = to_np(ops.gemm(w, a, residual=None if r is None else dev(r), forced_splits=S))
+            ref = O.project(codes, sc, group, 0, q, s, sm, 0, var, np.full(T, S, np.int32) if variant == "gemm" else S,
+                            residual=r)
+            assert_parity(got, ref, f"T={T} S={S} {variant} residual={r is not None}")
