@@ -43,6 +43,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace kxw4 {
 
@@ -103,6 +104,12 @@ struct G3Shape {
     static_assert(A_BYTES % 1024 == 0, "activation tile in whole 1 KB chunks");
     static_assert(S_LANES <= 64, "one scale load per wave and stage");
 };
+
+// f(integral_constant<int, I>) for each I of the sequence, in order
+template <class F, int... I>
+__device__ __forceinline__ void for_each_index(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
 
 // OCC: waves per SIMD the register budget is sized for
 template <int TA, int TB, int WMW, int WNW, int UNIT, int NST, int OCC>
@@ -365,9 +372,14 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     if (NST - 1 < NT) issue(NST - 1, NST - 1);
     read_next_step(0);
     // With one block per step every read is of the next step's stage, so the
-    // tracked offsets point there instead.
+    // tracked offsets point there instead. A one-block step whose ring fits
+    // the 16-bit offset field of an LDS read instead takes its stage as a
+    // compile-time index (the loop unrolled over the ring and the slot
+    // parity): the stage offset then folds into each read's immediate, and
+    // no offsets are moved at all.
     constexpr bool kTrackNext = TA * TB == 1;
-    if constexpr (kTrackNext) {
+    constexpr bool kStaticStage = NB == 1 && NST * STAGE <= 65536;
+    if constexpr (kTrackNext && !kStaticStage) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) ast[c] += STAGE;
         bst += STAGE;
@@ -386,10 +398,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
         for (int u = 0; u < UPS; ++u) w[jb][u] = 0.0f;
 
     int st = 0;
-    auto step = [&](const int kb, auto par) {
-        constexpr int PAR = decltype(par)::value;
-        const int stn = st == NST - 1 ? 0 : st + 1;
-        const int dn = (stn - st) * STAGE;
+    // (stc: the step's stage when compile-time, else -1 for the tracked one)
+    auto step = [&](const int kb, auto par, auto stc) {
+        constexpr int PAR = decltype(par)::value, SC = decltype(stc)::value;
+        const int sc = SC >= 0 ? SC : st;
+        const int stn = sc == NST - 1 ? 0 : sc + 1;
+        const int dn = (stn - sc) * STAGE;
+        // byte distances from the tracked offsets to this step's stage and
+        // to the next one
+        const int dcur = SC >= 0 ? SC * STAGE : 0;
+        const int dnext = SC >= 0 ? stn * STAGE : kTrackNext ? 0 : dn;
         const bool more = kb + 1 < NT;
 #pragma unroll
         for (int u = 0; u < UPS; ++u) wlast[u] = w[TB - 1][u];
@@ -404,7 +422,7 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
             if (b == NB - 1) {
                 if (more) {
                     arrive(kb + 1);
-                    if (kb + NST < NT) issue(kb + NST, st);
+                    if (kb + NST < NT) issue(kb + NST, sc);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -421,12 +439,12 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
             if (b == NB - 1) {
                 // the next step's first operands (after the last step: a
                 // harmless read of a stale stage)
-                read_next_step(kTrackNext ? 0 : dn);
+                read_next_step(dnext);
             } else {
-                if (jb == 0 && ib + 1 < TA) read_a(0, ib + 1, Anext);
+                if (jb == 0 && ib + 1 < TA) read_a(dcur, ib + 1, Anext);
                 if (ib == 0 && jb + 1 < TB) {
                     v4u wd[2];
-                    read_b(0, jb + 1, wd);
+                    read_b(dcur, jb + 1, wd);
                     unpack_b(wd, B[jb + 1]);
                 }
             }
@@ -459,28 +477,45 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        const int adv = kTrackNext ? ((stn == NST - 1 ? 0 : stn + 1) - stn) * STAGE : dn;
-        st = stn;
+        if constexpr (SC < 0) {
+            const int adv = kTrackNext ? ((stn == NST - 1 ? 0 : stn + 1) - stn) * STAGE : dn;
+            st = stn;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) ast[c] += adv;
-        bst += adv;
-        sst += adv;
+            for (int c = 0; c < 4; ++c) ast[c] += adv;
+            bst += adv;
+            sst += adv;
+        }
     };
+    using Dyn = std::integral_constant<int, -1>;
     // after the last step, its last block's updates
     constexpr int LAST0 = (NB - 1) & 1, LAST1 = (2 * NB - 1) & 1;
-    if constexpr (NB % 2 == 0) {
-        for (int kb = 0; kb < NT; ++kb) step(kb, std::integral_constant<int, 0>{});
+    if constexpr (kStaticStage) {
+        // U steps per iteration (a multiple of the ring and, for an odd
+        // block count, of the slot parity), then up to U - 1 more; step i of
+        // an iteration has stage i % NST and parity i % 2
+        constexpr int U = NB % 2 == 0 ? NST : (NST % 2 == 0 ? NST : 2 * NST);
+        int kb = 0;
+        auto one = [&](auto i) {
+            constexpr int I = decltype(i)::value;
+            step(kb + I, std::integral_constant<int, (NB & 1) * (I & 1)>{}, std::integral_constant<int, I % NST>{});
+        };
+        for (; kb + U <= NT; kb += U) for_each_index(one, std::make_integer_sequence<int, U>{});
+        for_each_index([&](auto i) { if (kb + decltype(i)::value < NT) one(i); }, std::make_integer_sequence<int, U - 1>{});
+        if (NB % 2 == 1 && ((NT - 1) & 1)) update(TA - 1, TB - 1, acc[LAST1], w[TB - 1]);
+        else update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+    } else if constexpr (NB % 2 == 0) {
+        for (int kb = 0; kb < NT; ++kb) step(kb, std::integral_constant<int, 0>{}, Dyn{});
         update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
     } else {
         // an odd block count flips the slot parity every step: two steps
         // per iteration keep the slots compile-time
         int kb = 0;
         for (; kb + 1 < NT; kb += 2) {
-            step(kb, std::integral_constant<int, 0>{});
-            step(kb + 1, std::integral_constant<int, 1>{});
+            step(kb, std::integral_constant<int, 0>{}, Dyn{});
+            step(kb + 1, std::integral_constant<int, 1>{}, Dyn{});
         }
         if (kb < NT) {
-            step(kb, std::integral_constant<int, 0>{});
+            step(kb, std::integral_constant<int, 0>{}, Dyn{});
             update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
         } else {
             update(TA - 1, TB - 1, acc[LAST1], w[TB - 1]);

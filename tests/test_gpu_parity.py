@@ -456,6 +456,17 @@ def test_gemm3_shapes(rows, K, T, group, gemm3_tile):
     assert_parity(got, ref, "bf16 + residual", bf16=True)
 
 
+@pytest.mark.parametrize("K", [128, 256, 384, 512, 768, 896, 1152, 1408])
+@pytest.mark.parametrize("tile", [8, 0])
+def test_gemm3_k_steps(K, tile):
+    # K step counts 1..11 at group 64: the one-block tile (8) unrolls its K
+    # loop over six steps (three ring stages x two slot parities) and
+    # finishes the rest one step at a time, so every remainder and counts
+    # below one iteration run; tile 0 is the default tracked-offset loop
+    with ops.option("gemm3_tile", tile):
+        test_gemm3_shapes([1040, 2064], K, 257, 64, tile)
+
+
 @pytest.mark.parametrize("rows,K,T,group", [
     # the tile chooser's own pick on ragged token counts
     ([1040, 2064], 640, 300, 128), ([4096], 512, 600, 128), ([1040], 1024, 1100, 64)])
