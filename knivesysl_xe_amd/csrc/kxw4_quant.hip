@@ -90,6 +90,32 @@ __device__ __forceinline__ int8_t quantize_one(float v, float s) {
     return (int8_t)(int)clampf(rintf(v / s), -127.0f, 127.0f);
 }
 
+// The element loops below take kQU elements per thread and pass: all kQU
+// loads are issued (at indices clamped into the row) before any is used, so a
+// pass costs one memory round trip instead of one per element; the values of
+// clamped positions are never used, and the arithmetic and its order are the
+// element loop's.
+constexpr int kQU = 8;
+
+// 1 / sqrt(mean(x^2) + eps) of row t, summed in a fixed order: thread tid
+// adds x[k]^2 for k = tid, tid + kQThreads, ... in turn, then the work-group
+// sum (the work-group must have kQThreads threads)
+__device__ __forceinline__ float row_rms_inv(const QuantArgs &a, int t, float *red) {
+    const int K = a.K, tid = threadIdx.x;
+    const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
+    float ss = 0.0f;
+    for (int k0 = tid; k0 < K; k0 += kQThreads * kQU) {
+        float x[kQU];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) x[u] = row[min(k0 + u * kQThreads, K - 1)];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u)
+            if (k0 + u * kQThreads < K) ss += x[u] * x[u];
+    }
+    ss = block_reduce_sum(ss, red);
+    return 1.0f / sqrtf(ss / (float)K + a.eps);
+}
+
 template <int P, bool PER_TOKEN>
 __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
     __shared__ float red[kQThreads / 64];
@@ -97,40 +123,51 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
     const int K = a.K;
     const int tid = threadIdx.x;
     float rms_inv = 0.0f;
-    if constexpr (P == kRmsNorm) {
-        const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
-        float ss = 0.0f;
-        for (int k = tid; k < K; k += kQThreads) ss += row[k] * row[k];
-        ss = block_reduce_sum(ss, red);
-        rms_inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
+    if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
     int8_t *qrow = a.q + (size_t)t * K;
     float s_tok = 1.0f;
     if constexpr (PER_TOKEN) {
         float mx = -INFINITY;
-        for (int k = tid; k < K; k += kQThreads) {
-            const float v = produce<P>(a, t, k, rms_inv);
-            if (a.out) a.out[(size_t)t * K + k] = v;
-            mx = fmaxf(mx, fabsf(v));
+        for (int k0 = tid; k0 < K; k0 += kQThreads * kQU) {
+            float v[kQU];
+#pragma unroll
+            for (int u = 0; u < kQU; ++u) v[u] = produce<P>(a, t, min(k0 + u * kQThreads, K - 1), rms_inv);
+#pragma unroll
+            for (int u = 0; u < kQU; ++u) {
+                const int k = k0 + u * kQThreads;
+                if (k < K) {
+                    if (a.out) a.out[(size_t)t * K + k] = v[u];
+                    mx = fmaxf(mx, fabsf(v[u]));
+                }
+            }
         }
         mx = block_reduce_max(mx, red);
         s_tok = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
         if (tid == 0) a.scale[t] = s_tok;
     }
-    // K % 32 == 0 and kQThreads % 32 == 0: each half wave walks whole blocks.
-    for (int k = tid; k < K; k += kQThreads) {
-        const float v = produce<P>(a, t, k, rms_inv);
-        float s = s_tok;
-        if constexpr (!PER_TOKEN) {
-            if (a.out) a.out[(size_t)t * K + k] = v;
-            const float mx = half_wave_max(fabsf(v));
-            s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
-            if ((k & 31) == 0) a.scale[(size_t)t * (K / 32) + (k >> 5)] = s;
+    // K % 32 == 0 and kQThreads % 32 == 0: each half wave walks whole blocks,
+    // so a half wave's positions are all in the row or all past it (those
+    // past it shuffle among themselves and store nothing).
+    for (int k0 = tid; k0 < K; k0 += kQThreads * kQU) {
+        float v[kQU];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) v[u] = produce<P>(a, t, min(k0 + u * kQThreads, K - 1), rms_inv);
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) {
+            const int k = k0 + u * kQThreads;
+            const bool in = k < K;
+            float s = s_tok;
+            if constexpr (!PER_TOKEN) {
+                if (a.out && in) a.out[(size_t)t * K + k] = v[u];
+                const float mx = half_wave_max(fabsf(v[u]));
+                s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+                if (in && (k & 31) == 0) a.scale[(size_t)t * (K / 32) + (k >> 5)] = s;
+            }
+            const int8_t q = quantize_one(v[u], s);
+            if (in) qrow[(k & ~63) + act_slot(k)] = q;
+            const int bsum = half_wave_sum((int)q);
+            if (in && (k & 31) == 0 && a.sum) a.sum[(size_t)t * (K / 32) + (k >> 5)] = bsum;
         }
-        const int8_t q = quantize_one(v, s);
-        qrow[(k & ~63) + act_slot(k)] = q;
-        const int bsum = half_wave_sum((int)q);
-        if ((k & 31) == 0 && a.sum) a.sum[(size_t)t * (K / 32) + (k >> 5)] = bsum;
     }
 }
 
@@ -149,24 +186,35 @@ __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
     const int nch = K / 8;
     float v[NCH][8];
     float mx = -INFINITY;
+    // Every chunk's load is issued before any is used, at an index clamped
+    // into the row (a chunk past the row reloads the last one and is not
+    // used): a load under its own `idx < nch` branch is followed by a full
+    // wait inside that branch, so the NCH loads would make NCH memory round
+    // trips one after another.
+    uint4 raw[P == kLoadBF16 ? NCH : 1];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int idx = tid + c * NT;
-        if (idx < nch) {
-            if constexpr (P == kLoadBF16) {
-                const uint4 x = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + (size_t)t * K)[idx];
-                const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+        const int idx = min(tid + c * NT, nch - 1);
+        if constexpr (P == kLoadBF16) {
+            raw[c] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + (size_t)t * K)[idx];
+        } else {
+            const float4 *row = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + (size_t)t * K);
+            const float4 x0 = row[2 * idx], x1 = row[2 * idx + 1];
+            v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
+            v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
+        }
+    }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v[c][2 * j] = __uint_as_float(w[j] << 16);
-                    v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-                }
-            } else {
-                const float4 *row = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + (size_t)t * K);
-                const float4 x0 = row[2 * idx], x1 = row[2 * idx + 1];
-                v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
-                v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
+    for (int c = 0; c < NCH; ++c) {
+        if constexpr (P == kLoadBF16) {
+            const uint32_t w[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[c][2 * j] = __uint_as_float(w[j] << 16);
+                v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
             }
+        }
+        if (tid + c * NT < nch) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
         }
@@ -207,6 +255,101 @@ __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
     }
 }
 
+// Reference mode (K32 blocks) in one pass: each thread holds chunks of 8
+// consecutive elements, so a K32 block is 4 consecutive lanes and its absmax
+// and code sum are two lane shuffles each (one element per lane would take
+// five dependent shuffles per reduction and element). Every chunk's inputs
+// are loaded before any is used, at chunk indices clamped into the row; the
+// per-element arithmetic is the element loop's (produce), and the codes of a
+// chunk are one 8-byte store in the slot order. RMSNorm keeps kQThreads
+// threads for its fixed-order row sum.
+template <int P, int NCH, int NT = kQThreads>
+__global__ __launch_bounds__(NT) void quantize_blk_kernel(QuantArgs a) {
+    static_assert(P != kRmsNorm || NT == kQThreads, "the row sum's order assumes kQThreads threads");
+    __shared__ float red[kQThreads / 64];
+    const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
+    const int nch = K / 8;
+    float rms_inv = 0.0f;
+    if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
+    const size_t row0 = (size_t)t * K;
+    float v[NCH][8];
+    uint4 raw[NCH][P == kLoadBF16 || P == kRmsNorm ? 1 : 2];
+    float4 upv[P == kSiluMul ? NCH : 1][2];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = min(tid + c * NT, nch - 1);
+        if constexpr (P == kLoadBF16) {
+            raw[c][0] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + row0)[idx];
+        } else {
+            const float4 *xr = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + row0);
+            const float4 x0 = xr[2 * idx], x1 = xr[2 * idx + 1];
+            v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
+            v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
+            if constexpr (P == kSiluMul) {
+                const float4 *ur = reinterpret_cast<const float4 *>(a.up + row0);
+                upv[c][0] = ur[2 * idx];
+                upv[c][1] = ur[2 * idx + 1];
+            }
+            if constexpr (P == kRmsNorm) raw[c][0] = reinterpret_cast<const uint4 *>(a.w)[idx];
+        }
+    }
+    int8_t *qrow = a.q + row0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = tid + c * NT;
+        // a K32 block's four chunks are all in the row or all past it
+        const bool in = idx < nch;
+        if constexpr (P == kLoadBF16) {
+            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[c][2 * j] = __uint_as_float(w[j] << 16);
+                v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+            }
+        } else if constexpr (P == kSiluMul) {
+            const float u[8] = {upv[c][0].x, upv[c][0].y, upv[c][0].z, upv[c][0].w,
+                                upv[c][1].x, upv[c][1].y, upv[c][1].z, upv[c][1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = (v[c][j] / (1.0f + expf(-v[c][j]))) * u[j];
+        } else if constexpr (P == kRmsNorm) {
+            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[c][2 * j] = v[c][2 * j] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] & 0xFFFFu)));
+                v[c][2 * j + 1] = v[c][2 * j + 1] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] >> 16)));
+            }
+        }
+        if (a.out && in) {
+            float4 *o = reinterpret_cast<float4 *>(a.out + row0) + 2 * idx;
+            o[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            o[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+        }
+        float mx = fabsf(v[c][0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const float sc = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+        uint32_t lo = 0, hi = 0;
+        int sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int8_t q = quantize_one(v[c][j], sc);
+            sum += q;
+            if (j < 4) lo |= (uint32_t)(uint8_t)q << (8 * j);
+            else hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
+        }
+        if (in) *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
+                    make_uint2(lo, hi);
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (in && (idx & 3) == 0) {
+            a.scale[(size_t)t * (K / 32) + (idx >> 2)] = sc;
+            if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
+        }
+    }
+}
+
 template <int P>
 static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
     if constexpr (P == kLoadF32 || P == kLoadBF16) {
@@ -235,6 +378,31 @@ static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
         }
     }
 general:
+    // (16-byte vector loads and stores of the rows, 8-byte code stores)
+    auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
+    if (block == 32 && a.K % 32 == 0 && al(a.x, 16) && al(a.up, 16) && al(a.w, 16) && al(a.out, 16) &&
+        al(a.q, 8)) {
+        const int nch = a.K / 8;
+        if constexpr (P != kRmsNorm) {
+            if (a.T < 64 && nch <= 3 * 1024) {
+                // few tokens: more threads per row, more loads in flight
+                if (nch <= 1024)
+                    hipLaunchKernelGGL((quantize_blk_kernel<P, 1, 1024>), dim3(a.T), dim3(1024), 0, st, a);
+                else
+                    hipLaunchKernelGGL((quantize_blk_kernel<P, 3, 1024>), dim3(a.T), dim3(1024), 0, st, a);
+                return hipGetLastError() == hipSuccess ? 0 : -6;
+            }
+        }
+        if (nch <= 10 * kQThreads) {
+            if (nch <= 2 * kQThreads)
+                hipLaunchKernelGGL((quantize_blk_kernel<P, 2>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            else if (nch <= 4 * kQThreads)
+                hipLaunchKernelGGL((quantize_blk_kernel<P, 4>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            else
+                hipLaunchKernelGGL((quantize_blk_kernel<P, 10>), dim3(a.T), dim3(kQThreads), 0, st, a);
+            return hipGetLastError() == hipSuccess ? 0 : -6;
+        }
+    }
     if (block == 32)
         hipLaunchKernelGGL((quantize_kernel<P, false>), dim3(a.T), dim3(kQThreads), 0, st, a);
     else
@@ -339,12 +507,15 @@ int launch_silu_mul_quant(float *out, const float *gate, const float *up, int T,
 __global__ __launch_bounds__(kQThreads) void rmsnorm_kernel(QuantArgs a) {
     __shared__ float red[kQThreads / 64];
     const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
-    const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
-    float ss = 0.0f;
-    for (int k = tid; k < K; k += kQThreads) ss += row[k] * row[k];
-    ss = block_reduce_sum(ss, red);
-    const float rms_inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-    for (int k = tid; k < K; k += kQThreads) a.out[(size_t)t * K + k] = produce<kRmsNorm>(a, t, k, rms_inv);
+    const float rms_inv = row_rms_inv(a, t, red);
+    for (int k0 = tid; k0 < K; k0 += kQThreads * kQU) {
+        float v[kQU];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) v[u] = produce<kRmsNorm>(a, t, min(k0 + u * kQThreads, K - 1), rms_inv);
+#pragma unroll
+        for (int u = 0; u < kQU; ++u)
+            if (k0 + u * kQThreads < K) a.out[(size_t)t * K + k0 + u * kQThreads] = v[u];
+    }
 }
 
 int launch_rmsnorm(float *out, const float *in, const uint16_t *w, int T, int H, float eps, hipStream_t st) {

@@ -148,6 +148,60 @@ def test_quantizer_bf16_input(block):
     assert np.array_equal(a.sum.cpu().numpy(), sm)
 
 
+@pytest.mark.parametrize("T,K", [
+    # every launch shape of the K32-block quantizer: 1024 threads with one or
+    # three chunks per thread (few tokens), 256 threads with 2, 4 or 10, and
+    # rows past 10 chunks per thread (the element loop)
+    (1, 4096), (2, 17408), (70, 4096), (64, 8192), (65, 20480), (64, 24576)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_quantizer_block_shapes(T, K, bf16):
+    rng = np.random.default_rng(T * 7 + K)
+    x = (rng.standard_normal((T, K)) * rng.uniform(0.01, 10, (T, 1))).astype(np.float32)
+    x[0, 64:96] = 0.0                                    # an all-zero block: scale 1
+    if bf16:
+        xb = workloads.f32_to_bf16_bits(x)
+        a = ops.quantize_act(dev(xb.view(np.int16)).view(torch.bfloat16), 32)
+        x = workloads.bf16_bits_to_f32(xb)
+    else:
+        a = ops.quantize_act(dev(x), 32)
+    q, s, sm = O.quantize_act(x, 32)
+    assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm)
+
+
+def test_quantizer_block_unaligned_rows():
+    # rows that do not start on 16 bytes take the element loop; same bits
+    T, K = 3, 4096
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    base = torch.zeros(T * K + 1, dtype=torch.float32, device=DEV)
+    xu = base[1:].view(T, K)
+    xu.copy_(dev(x))
+    assert xu.data_ptr() % 16 != 0
+    a = ops.quantize_act(xu, 32)
+    q, s, sm = O.quantize_act(x, 32)
+    assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm)
+
+
+@pytest.mark.parametrize("T,K", [(70, 4096), (1, 5120)])
+def test_silu_mul_quant_shapes(T, K):
+    # the K32-block SiLU quantizer at 256 and 1024 threads per row
+    rng = np.random.default_rng(T + K)
+    gate = (rng.uniform(-1, 1, (T, K)) * 8).astype(np.float32)
+    up = (rng.uniform(-1, 1, (T, K)) * 4).astype(np.float32)
+    hidden, a = ops.silu_mul_quant(dev(gate), dev(up), 32)
+    h = hidden.cpu().numpy()
+    ref = O.silu_mul(gate, up)
+    assert np.max(np.abs(h - ref) / (np.abs(ref) + 1e-30)) < 1e-5
+    q, s, sm = O.quantize_act(h, 32)
+    assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm)
+
+
 @pytest.mark.parametrize("block", [32, 0])
 def test_silu_mul_quant(block):
     # silu_quant_bench.cpp:40-55 inputs: scaled LCG draws plus zero blocks,
