@@ -171,6 +171,67 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
     }
 }
 
+// The values of this thread's NCH chunks of 8 consecutive elements of row t
+// (chunk tid + c*NT), every chunk's inputs loaded before any is used, at
+// chunk indices clamped into the row (a chunk past the row holds the last
+// chunk's values and is not used); the per-element arithmetic is produce's.
+template <int P, int NCH, int NT>
+__device__ __forceinline__ void chunk_values(const QuantArgs &a, int t, float rms_inv, float (&v)[NCH][8]) {
+    const int nch = a.K / 8, tid = threadIdx.x;
+    const size_t row0 = (size_t)t * a.K;
+    uint4 raw[NCH][P == kLoadBF16 || P == kRmsNorm ? 1 : 2];
+    float4 upv[P == kSiluMul ? NCH : 1][2];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = min(tid + c * NT, nch - 1);
+        if constexpr (P == kLoadBF16) {
+            raw[c][0] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + row0)[idx];
+        } else {
+            const float4 *xr = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + row0);
+            const float4 x0 = xr[2 * idx], x1 = xr[2 * idx + 1];
+            v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
+            v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
+            if constexpr (P == kSiluMul) {
+                const float4 *ur = reinterpret_cast<const float4 *>(a.up + row0);
+                upv[c][0] = ur[2 * idx];
+                upv[c][1] = ur[2 * idx + 1];
+            }
+            if constexpr (P == kRmsNorm) raw[c][0] = reinterpret_cast<const uint4 *>(a.w)[idx];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        if constexpr (P == kLoadBF16) {
+            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[c][2 * j] = __uint_as_float(w[j] << 16);
+                v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+            }
+        } else if constexpr (P == kSiluMul) {
+            const float u[8] = {upv[c][0].x, upv[c][0].y, upv[c][0].z, upv[c][0].w,
+                                upv[c][1].x, upv[c][1].y, upv[c][1].z, upv[c][1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = (v[c][j] / (1.0f + expf(-v[c][j]))) * u[j];
+        } else if constexpr (P == kRmsNorm) {
+            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[c][2 * j] = v[c][2 * j] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] & 0xFFFFu)));
+                v[c][2 * j + 1] = v[c][2 * j + 1] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] >> 16)));
+            }
+        }
+    }
+}
+
+// the producer's fp32 value of chunk idx, when the caller asked for it
+template <int NCH>
+__device__ __forceinline__ void store_chunk_out(const QuantArgs &a, int t, int idx, const float (&v)[8]) {
+    float4 *o = reinterpret_cast<float4 *>(a.out + (size_t)t * a.K) + 2 * idx;
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // Per-token mode with plain loads, one pass: each thread holds chunks of 8
 // consecutive elements (16-byte bf16 / 32-byte f32 loads) in registers for the
 // whole row, so the row is read once. The MFMA slot order keeps the 8 codes of
@@ -180,41 +241,19 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
 // shuffle.
 template <int P, int NCH, int NT = kQThreads>
 __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
-    static_assert(P == kLoadF32 || P == kLoadBF16, "plain loads");
+    static_assert(P != kRmsNorm || NT == kQThreads, "the row sum's order assumes kQThreads threads");
     __shared__ float red[NT / 64];
     const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
     const int nch = K / 8;
+    float rms_inv = 0.0f;
+    if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
     float v[NCH][8];
+    chunk_values<P, NCH, NT>(a, t, rms_inv, v);
     float mx = -INFINITY;
-    // Every chunk's load is issued before any is used, at an index clamped
-    // into the row (a chunk past the row reloads the last one and is not
-    // used): a load under its own `idx < nch` branch is followed by a full
-    // wait inside that branch, so the NCH loads would make NCH memory round
-    // trips one after another.
-    uint4 raw[P == kLoadBF16 ? NCH : 1];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int idx = min(tid + c * NT, nch - 1);
-        if constexpr (P == kLoadBF16) {
-            raw[c] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + (size_t)t * K)[idx];
-        } else {
-            const float4 *row = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + (size_t)t * K);
-            const float4 x0 = row[2 * idx], x1 = row[2 * idx + 1];
-            v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
-            v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        if constexpr (P == kLoadBF16) {
-            const uint32_t w[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[c][2 * j] = __uint_as_float(w[j] << 16);
-                v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-            }
-        }
         if (tid + c * NT < nch) {
+            if (P >= kSiluMul && a.out) store_chunk_out<NCH>(a, t, tid + c * NT, v[c]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
         }
@@ -273,57 +312,14 @@ __global__ __launch_bounds__(NT) void quantize_blk_kernel(QuantArgs a) {
     if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
     const size_t row0 = (size_t)t * K;
     float v[NCH][8];
-    uint4 raw[NCH][P == kLoadBF16 || P == kRmsNorm ? 1 : 2];
-    float4 upv[P == kSiluMul ? NCH : 1][2];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int idx = min(tid + c * NT, nch - 1);
-        if constexpr (P == kLoadBF16) {
-            raw[c][0] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + row0)[idx];
-        } else {
-            const float4 *xr = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + row0);
-            const float4 x0 = xr[2 * idx], x1 = xr[2 * idx + 1];
-            v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x0.z; v[c][3] = x0.w;
-            v[c][4] = x1.x; v[c][5] = x1.y; v[c][6] = x1.z; v[c][7] = x1.w;
-            if constexpr (P == kSiluMul) {
-                const float4 *ur = reinterpret_cast<const float4 *>(a.up + row0);
-                upv[c][0] = ur[2 * idx];
-                upv[c][1] = ur[2 * idx + 1];
-            }
-            if constexpr (P == kRmsNorm) raw[c][0] = reinterpret_cast<const uint4 *>(a.w)[idx];
-        }
-    }
+    chunk_values<P, NCH, NT>(a, t, rms_inv, v);
     int8_t *qrow = a.q + row0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int idx = tid + c * NT;
         // a K32 block's four chunks are all in the row or all past it
         const bool in = idx < nch;
-        if constexpr (P == kLoadBF16) {
-            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[c][2 * j] = __uint_as_float(w[j] << 16);
-                v[c][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-            }
-        } else if constexpr (P == kSiluMul) {
-            const float u[8] = {upv[c][0].x, upv[c][0].y, upv[c][0].z, upv[c][0].w,
-                                upv[c][1].x, upv[c][1].y, upv[c][1].z, upv[c][1].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[c][j] = (v[c][j] / (1.0f + expf(-v[c][j]))) * u[j];
-        } else if constexpr (P == kRmsNorm) {
-            const uint32_t w[4] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[c][2 * j] = v[c][2 * j] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] & 0xFFFFu)));
-                v[c][2 * j + 1] = v[c][2 * j + 1] * rms_inv * (1.0f + bf16_to_float((uint16_t)(w[j] >> 16)));
-            }
-        }
-        if (a.out && in) {
-            float4 *o = reinterpret_cast<float4 *>(a.out + row0) + 2 * idx;
-            o[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
-            o[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
-        }
+        if (a.out && in) store_chunk_out<NCH>(a, t, idx, v[c]);
         float mx = fabsf(v[c][0]);
 #pragma unroll
         for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
@@ -352,56 +348,40 @@ __global__ __launch_bounds__(NT) void quantize_blk_kernel(QuantArgs a) {
 
 template <int P>
 static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
-    if constexpr (P == kLoadF32 || P == kLoadBF16) {
-        // one pass with the row in registers, up to 20480 elements
-        const int nch = a.K / 8;
-        if (block != 32 && a.K % 32 == 0) {
-            // few tokens: a row's work-group is most of the launch, so it
-            // takes 1024 threads (three times the loads in flight per row;
-            // T=1, K=17408: 6.3 -> ~3 us)
-            if (a.T < 64 && nch <= 3 * 1024) {
-                if (nch <= 1024)
-                    hipLaunchKernelGGL((quantize_tok_kernel<P, 1, 1024>), dim3(a.T), dim3(1024), 0, st, a);
-                else
-                    hipLaunchKernelGGL((quantize_tok_kernel<P, 3, 1024>), dim3(a.T), dim3(1024), 0, st, a);
-                return hipGetLastError() == hipSuccess ? 0 : -6;
-            }
-            if (nch <= 2 * kQThreads)
-                hipLaunchKernelGGL((quantize_tok_kernel<P, 2>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            else if (nch <= 4 * kQThreads)
-                hipLaunchKernelGGL((quantize_tok_kernel<P, 4>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            else if (nch <= 10 * kQThreads)
-                hipLaunchKernelGGL((quantize_tok_kernel<P, 10>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            else
-                goto general;
-            return hipGetLastError() == hipSuccess ? 0 : -6;
-        }
-    }
-general:
-    // (16-byte vector loads and stores of the rows, 8-byte code stores)
+    // One pass with the row's chunks in registers, up to 20480 elements:
+    // per-token (block 0) on quantize_tok_kernel, K32 blocks on
+    // quantize_blk_kernel; 16-byte vector loads and stores of the rows and
+    // 8-byte code stores, so the rows must start on 16 bytes. With few
+    // tokens a row's work-group is most of the launch, so it takes 1024
+    // threads (more loads in flight per row; T=1, K=17408: 6.3 -> ~3 us);
+    // RMSNorm keeps 256 for its fixed-order row sum.
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
-    if (block == 32 && a.K % 32 == 0 && al(a.x, 16) && al(a.up, 16) && al(a.w, 16) && al(a.out, 16) &&
-        al(a.q, 8)) {
-        const int nch = a.K / 8;
-        if constexpr (P != kRmsNorm) {
-            if (a.T < 64 && nch <= 3 * 1024) {
-                // few tokens: more threads per row, more loads in flight
-                if (nch <= 1024)
-                    hipLaunchKernelGGL((quantize_blk_kernel<P, 1, 1024>), dim3(a.T), dim3(1024), 0, st, a);
-                else
-                    hipLaunchKernelGGL((quantize_blk_kernel<P, 3, 1024>), dim3(a.T), dim3(1024), 0, st, a);
-                return hipGetLastError() == hipSuccess ? 0 : -6;
+    const int nch = a.K / 8;
+    if (a.K % 32 == 0 && al(a.x, 16) && al(a.up, 16) && al(a.w, 16) && al(a.out, 16) && al(a.q, 8)) {
+        auto run = [&](auto kernel1024_1, auto kernel1024_3, auto kernel2, auto kernel4, auto kernel10) {
+            if (P != kRmsNorm && a.T < 64 && nch <= 3 * 1024) {
+                if (nch <= 1024) hipLaunchKernelGGL(kernel1024_1, dim3(a.T), dim3(1024), 0, st, a);
+                else hipLaunchKernelGGL(kernel1024_3, dim3(a.T), dim3(1024), 0, st, a);
+                return true;
             }
-        }
-        if (nch <= 10 * kQThreads) {
-            if (nch <= 2 * kQThreads)
-                hipLaunchKernelGGL((quantize_blk_kernel<P, 2>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            else if (nch <= 4 * kQThreads)
-                hipLaunchKernelGGL((quantize_blk_kernel<P, 4>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            else
-                hipLaunchKernelGGL((quantize_blk_kernel<P, 10>), dim3(a.T), dim3(kQThreads), 0, st, a);
-            return hipGetLastError() == hipSuccess ? 0 : -6;
-        }
+            if (nch > 10 * kQThreads) return false;
+            if (nch <= 2 * kQThreads) hipLaunchKernelGGL(kernel2, dim3(a.T), dim3(kQThreads), 0, st, a);
+            else if (nch <= 4 * kQThreads) hipLaunchKernelGGL(kernel4, dim3(a.T), dim3(kQThreads), 0, st, a);
+            else hipLaunchKernelGGL(kernel10, dim3(a.T), dim3(kQThreads), 0, st, a);
+            return true;
+        };
+        // (RMSNorm has no 1024-thread instances: the null pointers are never launched)
+        constexpr bool k1024 = P != kRmsNorm;
+        bool done;
+        if (block == 32)
+            done = run(k1024 ? quantize_blk_kernel<P, 1, k1024 ? 1024 : kQThreads> : nullptr,
+                       k1024 ? quantize_blk_kernel<P, 3, k1024 ? 1024 : kQThreads> : nullptr,
+                       quantize_blk_kernel<P, 2>, quantize_blk_kernel<P, 4>, quantize_blk_kernel<P, 10>);
+        else
+            done = run(k1024 ? quantize_tok_kernel<P, 1, k1024 ? 1024 : kQThreads> : nullptr,
+                       k1024 ? quantize_tok_kernel<P, 3, k1024 ? 1024 : kQThreads> : nullptr,
+                       quantize_tok_kernel<P, 2>, quantize_tok_kernel<P, 4>, quantize_tok_kernel<P, 10>);
+        if (done) return hipGetLastError() == hipSuccess ? 0 : -6;
     }
     if (block == 32)
         hipLaunchKernelGGL((quantize_kernel<P, false>), dim3(a.T), dim3(kQThreads), 0, st, a);

@@ -186,17 +186,19 @@ def test_quantizer_block_unaligned_rows():
     assert np.array_equal(a.sum.cpu().numpy(), sm)
 
 
-@pytest.mark.parametrize("T,K", [(70, 4096), (1, 5120)])
-def test_silu_mul_quant_shapes(T, K):
-    # the K32-block SiLU quantizer at 256 and 1024 threads per row
+@pytest.mark.parametrize("T,K", [(70, 4096), (1, 5120), (64, 20480)])
+@pytest.mark.parametrize("block", [32, 0])
+def test_silu_mul_quant_shapes(T, K, block):
+    # the SiLU quantizers at 256 and 1024 threads per row and 2 to 10 chunks
+    # per thread
     rng = np.random.default_rng(T + K)
     gate = (rng.uniform(-1, 1, (T, K)) * 8).astype(np.float32)
     up = (rng.uniform(-1, 1, (T, K)) * 4).astype(np.float32)
-    hidden, a = ops.silu_mul_quant(dev(gate), dev(up), 32)
+    hidden, a = ops.silu_mul_quant(dev(gate), dev(up), block)
     h = hidden.cpu().numpy()
     ref = O.silu_mul(gate, up)
     assert np.max(np.abs(h - ref) / (np.abs(ref) + 1e-30)) < 1e-5
-    q, s, sm = O.quantize_act(h, 32)
+    q, s, sm = O.quantize_act(h, block)
     assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
     assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
     assert np.array_equal(a.sum.cpu().numpy(), sm)
@@ -235,6 +237,26 @@ def test_rmsnorm_quant(block):
     for t in range(T):
         ref = O.rmsnorm(x[t], w, 1e-6)
         assert np.max(np.abs(nv[t] - ref)) <= 2e-6 * np.max(np.abs(ref))
+    q, s, sm = O.quantize_act(nv, block)
+    assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm)
+
+
+@pytest.mark.parametrize("T,H", [(70, 4096), (2, 17408), (1, 512)])
+@pytest.mark.parametrize("block", [32, 0])
+def test_rmsnorm_quant_shapes(T, H, block):
+    # the RMSNorm quantizers at 2, 4 and 10 chunks per thread
+    rng = np.random.default_rng(T * 3 + H)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = O.f32_to_bf16(rng.standard_normal(H).astype(np.float32) * 0.1)
+    normed, a = ops.rmsnorm_quant(dev(x), dev(w.view(np.int16)), 1e-6, block)
+    nv = normed.cpu().numpy()
+    for t in range(T):
+        ref = O.rmsnorm(x[t], w, 1e-6)
+        assert np.max(np.abs(nv[t] - ref)) <= 2e-6 * np.max(np.abs(ref))
+    y = ops.rmsnorm(dev(x), dev(w.view(np.int16)), 1e-6).cpu().numpy()
+    assert np.array_equal(nv.view(np.uint32), y.view(np.uint32))
     q, s, sm = O.quantize_act(nv, block)
     assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
     assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
