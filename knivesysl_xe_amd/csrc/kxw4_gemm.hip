@@ -81,37 +81,41 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     constexpr int ACH = BM * 8 / kGemmThreads;   // 16-byte activation chunks per thread
     v4i ra[ACH];
     v4u rb[2 * TB];
+    // The loads go out unconditionally, at token and row-group indices
+    // clamped into range, and the rows past T or M are zeroed when staged:
+    // a load under its own bounds branch is waited for inside the branch,
+    // which would hold every step's loads back until they arrive instead of
+    // leaving them in flight across the step.
     auto gload = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < ACH; ++i) {
             const int c = tid + kGemmThreads * i;
             const int row = c >> 3, col = c & 7;
-            const int t = t0 + row;
-            v4i v = {0, 0, 0, 0};
-            if (t < T) v = *reinterpret_cast<const v4i *>(a.q + (size_t)t * K + kb * kTileK + col * 16);
-            ra[i] = v;
+            const int t = min(t0 + row, T - 1);
+            ra[i] = *reinterpret_cast<const v4i *>(a.q + (size_t)t * K + kb * kTileK + col * 16);
         }
 #pragma unroll
         for (int i = 0; i < 2 * TB; ++i) {
             const int c = tid + kGemmThreads * i;
             const int rgl = c / (64 * TB), l = c % (64 * TB);
-            const int rg = rg0 + rgl;
-            v4u v = {0u, 0u, 0u, 0u};
-            if (rg < M / 16)
-                v = *reinterpret_cast<const v4u *>(W.codes + ((size_t)rg * NT + kb) * TILE + l * 16);
-            rb[i] = v;
+            const int rg = min(rg0 + rgl, M / 16 - 1);
+            rb[i] = *reinterpret_cast<const v4u *>(W.codes + ((size_t)rg * NT + kb) * TILE + l * 16);
         }
     };
     auto sstore = [&](int stage) {
 #pragma unroll
         for (int i = 0; i < ACH; ++i) {
             const int c = tid + kGemmThreads * i;
-            *reinterpret_cast<v4i *>(&As[stage][(c >> 3) * kApitch + (c & 7) * 16]) = ra[i];
+            const v4i zero = {0, 0, 0, 0};
+            *reinterpret_cast<v4i *>(&As[stage][(c >> 3) * kApitch + (c & 7) * 16]) =
+                t0 + (c >> 3) < T ? ra[i] : zero;
         }
 #pragma unroll
         for (int i = 0; i < 2 * TB; ++i) {
             const int c = tid + kGemmThreads * i;
-            *reinterpret_cast<v4u *>(&Bs[stage][(c / (64 * TB)) * TILE + (c % (64 * TB)) * 16]) = rb[i];
+            const v4u zero = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u *>(&Bs[stage][(c / (64 * TB)) * TILE + (c % (64 * TB)) * 16]) =
+                rg0 + c / (64 * TB) < M / 16 ? rb[i] : zero;
         }
     };
 
@@ -308,8 +312,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
     for (int kb = 0; kb < NT; ++kb) {
         const int stage = kb & 1;
         if (kb + 1 < NT) {
-            gload(kb + 1);
+            // (the scales first: a wait for them then leaves the tile
+            // loads issued after them in flight)
             load_scales(kb + 1, raw_nxt);
+            gload(kb + 1);
         }
         compute(stage, kb, raw_cur);
         if (kb + 1 < NT) {
