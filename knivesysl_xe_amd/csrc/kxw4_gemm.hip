@@ -199,19 +199,50 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs a) {
                 z[j] = zp ? sext4(raw[j]) : 0;
             }
         }
+        // Reference mode: the unit's activation scale and code sum of each of
+        // this lane's tokens, all loaded before any is used (a load under
+        // its own branch would be waited for before the next one went out,
+        // a memory round trip per token and unit). Every address is valid
+        // whichever the mode: the per-token scale index without K32 blocks,
+        // and the scale array (of the same [T][K/32] shape) standing in for
+        // the sums when the weights have no zero points; the values those
+        // modes do not use are replaced after the loads.
+        float asv[WM][4];
+        int smv[WM][4];
+        if constexpr (MODE != 0) {
+            const bool blk = a.block != 0, zps = a.scale_enc == 1;
+            const int32_t *sp = zps ? a.asum : reinterpret_cast<const int32_t *>(a.ascale);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = tw0 + i * 16 + 4 * g4 + r;
+                    const int tc = t < T ? t : 0;
+                    asv[i][r] = a.ascale[blk ? (size_t)tc * (K / 32) + u : (size_t)tc];
+                    int sm = 0;
+#pragma unroll
+                    for (int b = (u * UNIT) / 32; b < ((u + 1) * UNIT) / 32; ++b)
+                        sm += sp[(size_t)tc * (K / 32) + b];
+                    smv[i][r] = sm;
+                }
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    asv[i][r] = blk ? asv[i][r] : 1.0f;
+                    smv[i][r] = zps ? smv[i][r] : 0;
+                }
+        }
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = tw0 + i * 16 + 4 * g4 + r;
-                const int tc = t < T ? t : 0;
                 float as = 1.0f;
                 int sm = 0;
-                if (MODE != 0) {
-                    if (a.block != 0) as = a.ascale[(size_t)tc * (K / 32) + u];
-                    if (a.scale_enc == 1)
-                        for (int b = (u * UNIT) / 32; b < ((u + 1) * UNIT) / 32; ++b)
-                            sm += a.asum[(size_t)tc * (K / 32) + b];
+                if constexpr (MODE != 0) {
+                    as = asv[i][r];
+                    sm = smv[i][r];
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
