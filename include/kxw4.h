@@ -219,7 +219,9 @@ int kxw4_quantize_act_s4(const void *x, int x_dtype, int T, int K, uint8_t *q4,
  * K16 stage every token's activation row in one work-group's LDS: where T
  * rows do not fit (long K: at K = 17408 from T = 7 for W8, from 2-4 tokens
  * for K16 depending on M) the tokens run in chunks that do, each streaming
- * the weights again (same bits, more weight traffic). */
+ * the weights again (same bits, more weight traffic). W4 weights never
+ * chunk: a shape whose rows do not fit runs on the K-parallel kernel, which
+ * reads the weight once for all T tokens. */
 int kxw4_gemv(const kxw4_weight_t *w, const kxw4_act_t *a, void *y, int y_dtype,
               const float *residual, int splits, void *stream);
 
@@ -258,14 +260,13 @@ int kxw4_gemm_w4a4(const kxw4_weight_t *w, const uint8_t *q4, const float *scale
                    const int32_t *sum, int T, void *y, int y_dtype,
                    const float *residual, void *stream);
 
-/* No counterpart in the reference: an allocation-free x_gemv_w4a8 /
- * x_gemv_w4a8_add (kernels_dpas.cpp:1662-1680) for callers that cannot
- * allocate (code under HIP graph capture, tight serving loops). x[T][K]
- * (KXW4_F32 or KXW4_BF16) is quantized per K32 block into a fixed device
- * array of this library (640 KiB per GPU, held until the process ends), then
- * projected as kxw4_gemv with the default split plan, plus residual (may be
- * NULL). Limits: T in [1, 16], K <= 32768 (else -2). Allocates nothing;
- * calls that overlap on one GPU race on the array. */
+/* No counterpart in the reference. For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops): x[T][K] (KXW4_F32 or
+ * KXW4_BF16) is quantized per K32 block into a fixed device array of this
+ * library (640 KiB per GPU, held until the process ends), then projected as
+ * kxw4_gemv with the default split plan, plus residual (may be NULL).
+ * Limits: T in [1, 16], K <= 32768 (else -2). Allocates nothing; calls that
+ * overlap on one GPU race on the array. */
 int kxw4_gemv_x_noalloc(const kxw4_weight_t *w, const void *x, int x_dtype, int T, void *y,
                         int y_dtype, const float *residual, void *stream);
 

@@ -619,6 +619,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     };
     size_t lds = lds_for(a.T);
     if (lds > kRwLdsMax) {
+        // W4 weights hand the shape back: the K-parallel kernel reads the
+        // weight once for every token.
+        if (wf == kWfW4) return 1;
         // The tokens' activations do not fit (long K at W8 or K16, which
         // have no other kernel): run the tokens in chunks that do. A token's
         // outputs depend on its own activation row only, so the bits are the

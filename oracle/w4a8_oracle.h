@@ -47,8 +47,11 @@
  *   orc_e2m3         the OCP FP6 E2M3 closed form
  *   orc_e2m3_code_at parity unpinned beyond structure: tests show every
  *                    (row, col) owns a distinct contiguous 6-bit field of its
- *                    384-byte tile; the bit positions themselves restate
- *                    kernels_core.cpp:46-75 and no reference vector checks them
+ *                    384-byte tile, and that each lane's 16 codes are one
+ *                    little-endian 96-bit stream in its own 12 bytes (what
+ *                    kernels_core.cpp:55-57 states); the (row, col) ->
+ *                    (lane, index) map restates kernels_core.cpp:58-75 and no
+ *                    reference vector checks it
  *   orc_fit_int8     hand-derived known answers (tests/test_oracle.py):
  *                    a group whose scale moves in both refinements (one or
  *                    three refinements, or the negative side over 127, give
@@ -67,6 +70,20 @@
  *                    0 = separate multiply and add, the literal source. Both
  *                    are restated; which one Intel's compiled reference
  *                    produces is parity unpinned (no reference output pins it)
+ *   division         every division here (v/s in the quantizers, (hi-lo)/15
+ *                    and num/den in the fits, absmax/127) is IEEE correctly
+ *                    rounded. The reference is built with plain
+ *                    `icpx -fsycl -O2` (xpu/build.sh:13), whose default
+ *                    floating-point model may replace a division by a
+ *                    reciprocal approximation; which rounding Intel's
+ *                    compiled reference produces is parity unpinned
+ *   NaN in the GEMV  quantize_act_s8 reduces |v| with sycl::maximum
+ *   quantizer        (kernels_dpas.cpp:203-204), whose result on a NaN input
+ *                    depends on the sub-group's reduction order; the chunk
+ *                    quantizer takes a NaN-skipping fmax per lane first
+ *                    (1170-1172). The oracle applies fmax (NaN skipped) to
+ *                    both; the GEMV quantizer's NaN behaviour is parity
+ *                    unpinned (finite inputs are unaffected)
  */
 #ifndef W4A8_ORACLE_H
 #define W4A8_ORACLE_H

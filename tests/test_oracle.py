@@ -83,6 +83,61 @@ def test_e2m3_fragment_addressing_is_a_bijection():
     assert seen == set(range(512))
 
 
+def _plant_le(payload, tile_off, lane, idx, code):
+    """Write `code` as field `idx` of lane `lane`'s little-endian 96-bit
+    stream of 16 six-bit codes, in the lane's own 12 bytes of the tile
+    (kernels_core.cpp:55-57)."""
+    base = tile_off + 12 * lane
+    v = int.from_bytes(bytes(payload[base:base + 12]), "little")
+    v |= code << (6 * idx)
+    payload[base:base + 12] = np.frombuffer(v.to_bytes(12, "little"), np.uint8)
+
+
+def _lane_stream_holds(read, Kt=2, mt=1, kt=1, code=0b100101):
+    """One field at a time: the field planted as (lane, idx) of tile (mt, kt)
+    must be read back, with its value, at exactly one (row, col) of that
+    tile, every other position reading 0, and the 512 fields must land on
+    512 distinct positions. `code` is not its own 6-bit reversal."""
+    tile_off = (mt * Kt + kt) * 384
+    where = set()
+    for lane in range(32):
+        for idx in range(16):
+            payload = np.zeros(2 * Kt * 384, np.uint8)
+            _plant_le(payload, tile_off, lane, idx, code)
+            hits = [(r, c, read(payload, Kt, 16 * mt + r, 32 * kt + c))
+                    for r in range(16) for c in range(32)]
+            nz = [h for h in hits if h[2] != 0]
+            if len(nz) != 1 or nz[0][2] != code:
+                return False
+            where.add(nz[0][:2])
+    return len(where) == 512
+
+
+def _oracle_read(payload, Kt, row, col):
+    return O.lib().orc_e2m3_code_at(payload.ctypes.data, Kt, row, col)
+
+
+def _mutant_read(big_endian, stride):
+    # the oracle's (row, col) -> (lane, idx) map, read from another stream
+    # convention: most significant field first, or a 16-byte lane stride
+    def read(payload, Kt, row, col):
+        lane = (((row & 15) >> 1) << 2) | ((col & 31) >> 3)
+        idx = (((col >> 2) & 1) << 3) | ((row & 1) << 2) | (col & 3)
+        base = ((row >> 4) * Kt + (col >> 5)) * 384 + lane * stride
+        v = int.from_bytes(bytes(payload[base:base + 12]), "big" if big_endian else "little")
+        return (v >> (6 * (15 - idx) if big_endian else 6 * idx)) & 0x3F
+    return read
+
+
+def test_e2m3_lanes_are_little_endian_12_byte_streams():
+    assert _lane_stream_holds(_oracle_read)
+    # the check discriminates: a big-endian stream or a 16-byte lane stride
+    # (the other plausible readings of the payload) fail it
+    assert _lane_stream_holds(_mutant_read(False, 12))
+    assert not _lane_stream_holds(_mutant_read(True, 12))
+    assert not _lane_stream_holds(_mutant_read(False, 16))
+
+
 # ------------------------------------------------------------------ quantizer
 @pytest.mark.parametrize("mode", ["finite", "exceptional"])
 @pytest.mark.parametrize("block", [32, 0])

@@ -130,6 +130,50 @@ def test_noalloc_matches_x_gemv_w4a8(group):
         assert np.array_equal(bits(got_add), bits(y_add)), f"x_gemv_w4a8_add M={M} K={K}"
 
 
+# multi-token cases checked against the CPU oracle itself: the longest K at
+# the most tokens (group 64, where the W4 activations exceed one work-group's
+# LDS and the K-parallel kernel runs), and T > 1 on the W8 and K16 tiers
+ORACLE_CASES = [
+    (5120, 17408, 64, _lib.SCALE_FP16_ZP4, 16),
+    (2048, 4096, 32, _lib.SCALE_W8, 8),
+    (1024, 5120, 16, _lib.SCALE_FP16_ZP4, 5),
+]
+
+
+@pytest.mark.parametrize("M,K,group,enc,T", ORACLE_CASES)
+def test_noalloc_multi_token_matches_oracle(M, K, group, enc, T):
+    from oracle import oracle as O
+    O.set_num_threads(16)
+    print(f"noalloc vs oracle M={M} K={K} group={group} enc={enc} T={T}", flush=True)
+    rng = np.random.default_rng(M + K + T)
+    if enc == _lib.SCALE_W8:
+        codes = rng.integers(-128, 128, (M, K)).astype(np.int8)
+        sc = (np.abs(rng.standard_normal((M, K // 32))) * 0.002).astype(np.float16).view(np.uint16)
+        w = ops.W4Weight.from_codes_s8(torch.from_numpy(codes).cuda(),
+                                       torch.from_numpy(sc.view(np.int16)).cuda())
+        o_enc = O.SCALE_S8
+    else:
+        codes = rng.integers(-8, 8, (M, K)).astype(np.int8)
+        sc = (np.abs(rng.standard_normal((M, K // group))) * 0.02).astype(np.float16).view(np.uint16)
+        sc = ((sc & 0xFFF0) | (rng.integers(-8, 8, sc.shape) & 0xF)).astype(np.uint16)
+        w = ops.W4Weight.from_codes(torch.from_numpy(codes).cuda(),
+                                    torch.from_numpy(sc.view(np.int16)).cuda(), group, enc)
+        o_enc = O.SCALE_FP16_ZP4
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    res = rng.standard_normal((T, M)).astype(np.float32)
+    q, s, sm = O.quantize_act(x, 32)
+    S = O.gemv_splits(M // 16)
+    for r in (None, res):
+        got = noalloc(w, torch.from_numpy(x).cuda(), None if r is None else torch.from_numpy(r).cuda())
+        torch.cuda.synchronize()
+        want = O.project(codes, sc, group, o_enc, q, s, sm, 32, O.VAR_GEMV, S, residual=r)
+        g = got.cpu().numpy()
+        rel = np.max(np.abs(g.astype(np.float64) - want) / (np.abs(want.astype(np.float64)) + 1e-3))
+        assert rel <= 1e-3, f"M={M} K={K} T={T} residual={r is not None}: max rel {rel}"
+        assert np.array_equal(g.view(np.uint32), want.view(np.uint32)), \
+            f"M={M} K={K} T={T} residual={r is not None}: not bit-exact"
+
+
 def test_noalloc_limits_and_arguments():
     rng = np.random.default_rng(5)
     L = _lib.lib()
