@@ -418,10 +418,13 @@ static void launch_w8(const GemmArgs &a, bool splits, bool debug, dim3 grid, hip
 }
 
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st) {
-    // The per-token, one-split mode goes to the large-tile kernel; the
-    // gemm_kernel option keeps it here (the tests cover both).
+    // The one-split modes go to the large-tile kernels (per-token: gemm3;
+    // K32 activation blocks: gemmr); the gemm_kernel option keeps them here
+    // (the tests cover both).
     if (!debug && options().gemm_kernel != kGemmGeneral && !a.w8) {
-        const int r = launch_gemm3(a, st);
+        int r = launch_gemm3(a, st);
+        if (r != 1) return r;
+        r = launch_gemmr(a, st);
         if (r != 1) return r;
     }
     bool splits = false;

@@ -113,6 +113,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st);
 int launch_gemm(GemmArgs &a, bool debug, hipStream_t st);
 // Returns 1 (nothing launched) outside the per-token, one-split-per-token mode.
 int launch_gemm3(GemmArgs &a, hipStream_t st);
+// Returns 1 (nothing launched) outside the reference mode (K32 activation
+// blocks, W4 codes) with one split per token.
+int launch_gemmr(GemmArgs &a, hipStream_t st);
 
 // Kernel-selection options (kxw4_set_option): process-wide, read by the
 // launchers. Defaults select the kernels measured fastest; the others keep
@@ -127,6 +130,7 @@ struct Options {
     int rowwave_k = 0;                // KXW4_ROWWAVE_K: work-groups per CU, 0 = launcher's plan
     int gemm_kernel = kGemmAuto;      // KXW4_GEMM_KERNEL: auto / general
     int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..9, -1 = cost model
+    int gemmr_tile = -1;              // KXW4_GEMMR_TILE: 0..8, -1 = default
     int w4a4_tile = -1;               // KXW4_W4A4_TILE: 0..4, -1 = default rule
 };
 const Options &options();

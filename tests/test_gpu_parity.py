@@ -550,6 +550,61 @@ def test_gemm3_auto_tile(rows, K, T, group):
     test_gemm3_shapes(rows, K, T, group, None)
 
 
+@pytest.fixture(params=list(range(9)))
+def gemmr_tile(request):
+    # every tile configuration of the reference-mode large-tile kernel
+    with ops.option("gemmr_tile", request.param):
+        yield request.param
+
+
+@pytest.mark.parametrize("rows,K,T,group,enc", [
+    # x_gemm_w4a8's own inputs (K32 activation blocks, FP16|zp K32 and K64
+    # weights) and plain FP16 weights at every group size; partial token
+    # and row tiles, fan-out weights of different heights, fewer K steps
+    # than ring stages, rows that start a new scale group mid-step
+    ([1040], 1024, 300, 32, 1), ([1040, 2064], 640, 257, 64, 1), ([4096], 128, 520, 32, 1),
+    ([256], 5120, 2048, 64, 1), ([1040], 512, 300, 32, 0), ([528, 1040], 1024, 520, 64, 0),
+    ([1024], 768, 400, 128, 0)])
+def test_gemmr_shapes(rows, K, T, group, enc, gemmr_tile):
+    print(f"gemmr rows={rows} K={K} T={T} group={group} enc={enc} tile={gemmr_tile}", flush=True)
+    rng = np.random.default_rng(sum(rows) + K + T + enc)
+    wts = [rand_weight(rng, M, K, group, enc) for M in rows]
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    x[:, :32] = 0.0                                  # an all-zero block (scale 1)
+    res = rng.standard_normal((T, rows[0])).astype(np.float32)
+    a = ops.quantize_act(dev(x), 32)
+    q, s, sm = O.quantize_act(x, 32)
+    ws = [weight(c, sc, group, enc) for c, sc in wts]
+    sps = [O.segment_splits(T, M, K) for M in rows]
+    assert all(np.all(sp == 1) for sp in sps)       # the shapes the kernel takes
+    ys = ops.gemm_fanout(ws, a, torch.float32)
+    for i, ((c, sc), y, sp) in enumerate(zip(wts, ys, sps)):
+        ref = O.project(c, sc, group, enc, q, s, sm, 32, O.VAR_GEMM, sp)
+        assert_parity(to_np(y), ref, f"weight {i} rows={rows[i]}")
+    got = to_np(ops.gemm(ws[0], a, torch.bfloat16, residual=dev(res)))
+    ref = O.project(*wts[0], group, enc, q, s, sm, 32, O.VAR_GEMM, sps[0], residual=res, out_bf16=True)
+    assert_parity(got, ref, "bf16 + residual", bf16=True)
+
+
+def test_gemmr_packed_segments(gemmr_tile):
+    # packed prefill segments whose split plans are all 1 (ragged lengths):
+    # rows are independent of the segments, so the packed launch equals the
+    # oracle per segment
+    rng = np.random.default_rng(11)
+    M, K, group = 8192, 512, 32
+    offs = np.array([0, 25, 89, 389, 600], np.int32)
+    T = int(offs[-1])
+    c, sc = rand_weight(rng, M, K, group, 1)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    a = ops.quantize_act(dev(x), 32)
+    q, s, sm = O.quantize_act(x, 32)
+    sp = O.segment_splits(T, M, K, offs)
+    assert np.all(sp == 1)
+    got = to_np(ops.gemm(weight(c, sc, group, 1), a, offsets=offs))
+    ref = O.project(c, sc, group, 1, q, s, sm, 32, O.VAR_GEMM, sp)
+    assert_parity(got, ref, "packed reference-mode segments")
+
+
 @pytest.mark.parametrize("name", ["cfg2_m512", "cfg3"])
 def test_baseline_config_gemm_general(name, gemm_general):
     run_config(name)
