@@ -104,7 +104,7 @@ const char *kxw4_error_string(int code);
  *   rowwave_ring       8 = eight weight tiles in flight per wave (else 4)
  *   gemm_kernel        0 auto, 1 the general GEMM for every prefill shape
  *   gemm3_tile         -1 cost model, 0..9 one 32x32x32 GEMM tile
- *   gemmr_tile         -1 default, 0..8 one reference-mode (K32 activation
+ *   gemmr_tile         -1 default, 0..9 one reference-mode (K32 activation
  *                      block) GEMM tile
  *   w4a4_tile          -1 default rule, 0..4 one W4A4 GEMM tile
  * Returns 0, -1 for an unknown name, -2 for a value out of range; *previous

@@ -25,7 +25,7 @@ const OptionDesc kOptions[] = {
     {"rowwave_spw", &Options::rowwave_spw, 0, 16},
     {"gemm_kernel", &Options::gemm_kernel, kGemmAuto, kGemmGeneral},
     {"gemm3_tile", &Options::gemm3_tile, -1, 9},
-    {"gemmr_tile", &Options::gemmr_tile, -1, 8},
+    {"gemmr_tile", &Options::gemmr_tile, -1, 9},
     {"w4a4_tile", &Options::w4a4_tile, -1, 4},
     {"rowwave_ring", &Options::rowwave_ring, 0, 8},
     {"rowwave_k", &Options::rowwave_k, 0, 64},
@@ -50,7 +50,7 @@ Options from_env() {
     if (const char *e = getenv("KXW4_GEMM_KERNEL"))
         if (!strcmp(e, "general")) o.gemm_kernel = kGemmGeneral;
     num("KXW4_GEMM3_TILE", -1, 9, o.gemm3_tile);
-    num("KXW4_GEMMR_TILE", -1, 8, o.gemmr_tile);
+    num("KXW4_GEMMR_TILE", -1, 9, o.gemmr_tile);
     num("KXW4_W4A4_TILE", -1, 4, o.w4a4_tile);
     return o;
 }

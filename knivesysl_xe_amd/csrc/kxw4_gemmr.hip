@@ -40,25 +40,28 @@ constexpr int kGrGroupTT = 4;      // token tiles per raster group
 
 #define KXW4_GR_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
-// Four int8 bytes w - z from four nibbles held as w + 8 (the packed dword
-// XOR 0x88888888, masked to one nibble per byte); c = (120 - z) * 0x01010101.
-// The byte sums w + 128 - z stay in [113, 143], so no carry crosses a byte,
-// and the XOR turns the excess-128 bytes into two's complement.
-__device__ __forceinline__ uint32_t gr_zp_bytes(uint32_t u, uint32_t c) { return (u + c) ^ 0x80808080u; }
-
 // A operand of one K32 unit: dword d0 of lane group 2kg (K slots 0..7) and
-// d1 of lane group 2kg + 1 (slots 8..15), unpacked to w - z (ZP) or 16 w.
+// d1 of lane group 2kg + 1 (slots 8..15), unpacked to the bytes w - z (ZP)
+// or 16 w. With zero points: each nibble n (two's complement w) becomes the
+// byte 0x80 | (n ^ 8) = 128 + w + 8 (one bit operation); subtracting
+// zz = (z + 8) * 0x01010101 leaves 128 + w - z in [113, 143] per byte, so no
+// borrow crosses a byte, and the XOR turns the excess-128 bytes into two's
+// complement.
+__device__ __forceinline__ uint32_t gr_zp_bytes(uint32_t nib, uint32_t zz) {
+    const uint32_t e = ((nib ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u;
+    return (e - zz) ^ 0x80808080u;
+}
+
 template <bool ZP>
-__device__ __forceinline__ v4i gr_unpack(uint32_t d0, uint32_t d1, uint32_t c) {
+__device__ __forceinline__ v4i gr_unpack(uint32_t d0, uint32_t d1, uint32_t zz) {
     v4i b;
     if constexpr (ZP) {
-        const uint32_t x0 = d0 ^ 0x88888888u, x1 = d1 ^ 0x88888888u;
-        b.x = (int)gr_zp_bytes(x0 & 0x0F0F0F0Fu, c);
-        b.y = (int)gr_zp_bytes((x0 >> 4) & 0x0F0F0F0Fu, c);
-        b.z = (int)gr_zp_bytes(x1 & 0x0F0F0F0Fu, c);
-        b.w = (int)gr_zp_bytes((x1 >> 4) & 0x0F0F0F0Fu, c);
+        b.x = (int)gr_zp_bytes(d0, zz);
+        b.y = (int)gr_zp_bytes(d0 >> 4, zz);
+        b.z = (int)gr_zp_bytes(d1, zz);
+        b.w = (int)gr_zp_bytes(d1 >> 4, zz);
     } else {
-        (void)c;
+        (void)zz;
         b.x = (int)nib_lo16(d0);
         b.y = (int)nib_hi16(d0);
         b.z = (int)nib_lo16(d1);
@@ -82,7 +85,12 @@ struct GrShape {
     static constexpr int W_OFF = A_BYTES;
     static constexpr int S_OFF = W_OFF + W_BYTES;
     static constexpr int AS_OFF = (S_OFF + S_BYTES + 15) / 16 * 16;
-    static constexpr int STAGE = (AS_OFF + AS_BYTES + 1023) / 1024 * 1024;
+    // prepared once per stage by the waves that loaded the scales: the FP16
+    // scales with the zero-point nibble cleared ([row-group][group][16]
+    // u16) and the zero-point bytes z + 8 ([row-group][group][16] u8)
+    static constexpr int MS_OFF = AS_OFF + AS_BYTES;
+    static constexpr int ZZ_OFF = MS_OFF + S_BYTES;
+    static constexpr int STAGE = (ZZ_OFF + S_BYTES / 2 + 1023) / 1024 * 1024;
     // loads per wave and stage, equal for every wave (one vmcnt retires a
     // stage); chunk indices wrap when the waves do not divide them, and a
     // few chunks are then loaded twice (same bytes to the same LDS address)
@@ -96,7 +104,8 @@ struct GrShape {
         return d;
     }
     static constexpr int S_LANES = s_lanes();
-    static constexpr int AS_CHUNKS = BM / 64;            // 64 tokens x 16 bytes per load
+    static constexpr int AS_LANES = BM < 64 ? BM : 64;   // tokens (16 bytes each) per load
+    static constexpr int AS_CHUNKS = BM / AS_LANES;
     static constexpr int AS_LOADS = (AS_CHUNKS + NW - 1) / NW;
     static constexpr int LOADS = A_LOADS + W_LOADS + 1 + AS_LOADS;
     // output staging: one token block of a wave at a time, [token][row]
@@ -105,7 +114,7 @@ struct GrShape {
     static constexpr int SLAB = 32 * EPS * 4;
     template <int NST>
     static constexpr int lds_bytes() { return NST * STAGE > NW * SLAB ? NST * STAGE : NW * SLAB; }
-    static_assert(A_BYTES % 1024 == 0 && BM % 64 == 0, "activation tile in whole 1 KB chunks");
+    static_assert(A_BYTES % 1024 == 0 && BM % AS_LANES == 0, "activation tile in whole 1 KB chunks");
     static_assert(S_LANES <= 64, "one scale load per wave and stage");
 };
 
@@ -115,8 +124,8 @@ __global__ __launch_bounds__(64 * WR * WT)
 __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs a) {
     using S = GrShape<NT, WR, WT, GROUP>;
     constexpr int NW = S::NW, BM = S::BM, RGS = S::RGS, GPS = S::GPS, STAGE = S::STAGE;
-    // four or more waves per SIMD: the lean pipeline (one MFMA result live)
-    constexpr bool LEAN = OCC >= 4;
+    // five or more waves per SIMD: the lean pipeline (one MFMA result live)
+    constexpr bool LEAN = OCC >= 5;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     // ---- block -> (token tile, weight, n-tile), XCD-aware raster: the
@@ -167,7 +176,7 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs 
         return ((uint32_t)rg * G + g) * 32 + half * 16;      // bytes
     };
     auto as_off = [&](int ln, int i) {
-        const int t = ((wave + NW * i) % S::AS_CHUNKS) * 64 + ln;
+        const int t = ((wave + NW * i) % S::AS_CHUNKS) * S::AS_LANES + min(ln, S::AS_LANES - 1);
         return (uint32_t)min(t0 + t, T - 1) * KB * 4;        // bytes
     };
     const uint8_t *qg = reinterpret_cast<const uint8_t *>(a.q);
@@ -192,11 +201,14 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs 
             __builtin_amdgcn_global_load_lds((const void *)(sg + (size_t)kb * GPS * 32 + s_off(ln)),
                                              KXW4_GR_LDS(base + S::S_OFF + (wave * S::S_LANES) % S::S_TOTAL * 16),
                                              16, 0, 0);
+        // (lanes past a partial load's tokens are masked off; the load
+        // still counts once in vmcnt)
 #pragma unroll
         for (int i = 0; i < S::AS_LOADS; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(ag + (size_t)kb * 16 + as_off(ln, i)),
-                                             KXW4_GR_LDS(base + S::AS_OFF + ((wave + NW * i) % S::AS_CHUNKS) * 1024),
-                                             16, 0, 0);
+            if (S::AS_LANES == 64 || lane < S::AS_LANES)
+                __builtin_amdgcn_global_load_lds((const void *)(ag + (size_t)kb * 16 + as_off(ln, i)),
+                                                 KXW4_GR_LDS(base + S::AS_OFF + ((wave + NW * i) % S::AS_CHUNKS) * S::AS_LANES * 16),
+                                                 16, 0, 0);
     };
 
     // ---- per-lane read offsets: lane = weight row / token m of a block,
@@ -204,10 +216,10 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs 
     const int m = lane & 31, kg = lane >> 5;
     const int rgl = 2 * wr + (m >> 4);                       // tile row-group of this lane's operand row
     const int w_lds = S::W_OFF + rgl * kTileBytes + (32 * kg + (m & 15)) * 16;
-    const int z_lds = S::S_OFF + rgl * GPS * 32 + (m & 15) * 2;
+    const int zz_lds = S::ZZ_OFF + rgl * GPS * 16 + (m & 15);
     // weight scales of this lane's output rows 8q + 4kg + e (e = 0..3) of
     // the wave's row block: row-group 2wr + q/2, rows 8(q%2) + 4kg + e
-    const int ws_lds = S::S_OFF + 2 * wr * GPS * 32 + 8 * kg;   // + (q/2) GPS 32 + (q%2) 16
+    const int ws_lds = (ZP ? S::MS_OFF : S::S_OFF) + 2 * wr * GPS * 32 + 8 * kg;   // + (q/2) GPS 32 + (q%2) 16
     // activation pieces of token block j: row tb + m, pieces 4c + 2kg + {0,1}
     const int tb = wt * NT * 32;                             // first token of this wave in the tile
     const int tsw = ((tb + m) >> 1) & 7;                     // the row's swizzle (tb is a multiple of 32)
@@ -226,30 +238,54 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs 
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
         if (s < NTK) issue(s, s);
+    // Step kb reads stage kb % NST. (Unrolling the K loop over the ring, so
+    // that the stage is a compile-time index, makes every instance with a
+    // ring under 64 KB spill.)
     int st = 0;
     for (int kb = 0; kb < NTK; ++kb) {
         const int later = min(NST - 2, NTK - 1 - kb);
         if (NST >= 4 && later >= 2) KXW4_WAIT_VMCNT(2 * LD);
         else if (NST >= 3 && later >= 1) KXW4_WAIT_VMCNT(LD);
         else KXW4_WAIT_VMCNT(0);
+        const uint8_t *sb = smem + st * STAGE;
+        if constexpr (ZP) {
+            // the scale granules this wave loaded into the stage (8 rows of
+            // one row-group and scale group each): masked scales and
+            // zero-point bytes, published by the barrier below (written to
+            // their own regions, so a granule two waves loaded is prepared
+            // twice with the same values)
+            if (lane < S::S_LANES) {
+                const int gi = (wave * S::S_LANES) % S::S_TOTAL + lane;
+                const v4u p = *reinterpret_cast<const v4u *>(sb + S::S_OFF + gi * 16);
+                v4u ms;
+                ms.x = p.x & 0xFFF0FFF0u;
+                ms.y = p.y & 0xFFF0FFF0u;
+                ms.z = p.z & 0xFFF0FFF0u;
+                ms.w = p.w & 0xFFF0FFF0u;
+                *reinterpret_cast<v4u *>(const_cast<uint8_t *>(sb) + S::MS_OFF + gi * 16) = ms;
+                // z + 8 = (p & 15) ^ 8 of each row, one byte per row: bytes
+                // 0 and 2 of each dword pair up with the two rows it holds
+                uint2 zb;
+                zb.x = __builtin_amdgcn_perm(p.y, p.x, 0x06040200u) & 0x0F0F0F0Fu;
+                zb.y = __builtin_amdgcn_perm(p.w, p.z, 0x06040200u) & 0x0F0F0F0Fu;
+                zb.x ^= 0x08080808u;
+                zb.y ^= 0x08080808u;
+                *reinterpret_cast<uint2 *>(const_cast<uint8_t *>(sb) + S::ZZ_OFF + gi * 8) = zb;
+            }
+        }
         lds_sync_after_dma();
         if (kb + NST - 1 < NTK) issue(kb + NST - 1, st == 0 ? NST - 1 : st - 1);
-        const uint8_t *sb = smem + st * STAGE;
         // The step is I = 4 NT items (unit u, token block j), j fastest, run
         // as a software pipeline: item i + 2's operands are read from LDS
         // and item i + 1's MFMA issued before item i's chain updates, so the
         // chain runs while the matrix core works and only two MFMA results
         // are live.
         constexpr int I = 4 * NT;
-        // zero-point bytes (120 - z) * 0x01010101 of the operand row for
-        // scale group g: 128 - ((p & 15) ^ 8), replicated to every byte
+        // zero-point bytes (z + 8) * 0x01010101 of the operand row for
+        // scale group g
         auto zc_of = [&](int g) -> uint32_t {
-            if constexpr (ZP) {
-                const uint32_t p = *reinterpret_cast<const uint16_t *>(sb + z_lds + g * 32);
-                return __builtin_amdgcn_perm(0u, 128u - ((p & 15u) ^ 8u), 0u);
-            } else {
-                return 0u;
-            }
+            if constexpr (ZP) return __builtin_amdgcn_perm(0u, (uint32_t)*(sb + zz_lds + g * 16), 0u);
+            else return 0u;
         };
         // the step's packed weight dwords of this lane's operand row: dword
         // u of lane groups 2kg (wd0) and 2kg + 1 (wd1) is unit u (the lean
@@ -268,9 +304,8 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemmr_kernel(const GemmArgs 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint2 v = *reinterpret_cast<const uint2 *>(sb + ws_lds + (q >> 1) * GPS * 32 + (q & 1) * 16 + g * 32);
-                const uint32_t mask = ZP ? 0xFFF0FFF0u : 0xFFFFFFFFu;
-                w[2 * q] = v.x & mask;
-                w[2 * q + 1] = v.y & mask;
+                w[2 * q] = v.x;
+                w[2 * q + 1] = v.y;
             }
         };
         // item i's activation operand (this unit's 8 bytes of pieces
@@ -452,14 +487,16 @@ static int launch_gr(GemmArgs &a, hipStream_t st) {
 // SIMD's VALU issue, so what decides is how evenly the 32x32 blocks spread
 // over the SIMDs and how many waves share a SIMD (graph replay, bit-exact,
 // T=2048 K=N=5120 group 32 / T=512 K=17408 N=5120 group 64):
-//   4 (default): 128 x 64, 4 waves of 2 token blocks, three work-groups per
-//     CU: 217 / 325 us;
+//   4: 128 x 64, 4 waves of 2 token blocks, four work-groups per CU:
+//     205 / 315 us (the default while its grid gives every CU at least
+//     three work-groups);
+//   9: 128 x 32, 4 waves of one token block, five work-groups per CU:
+//     226 / 277 us (the default for smaller grids);
 //   0: 160 x 256, 10 waves of 4 token blocks (3, 3, 2, 2 per SIMD), one
-//     work-group per CU: 234 / 757 us (the T=512 grid fills a quarter of the
-//     CUs);
-//   5: 160 x 64, 10 waves of one token block: 384 / 319 us;
+//     work-group per CU: 230 / 760 us;
+//   5: 160 x 64, 10 waves of one token block: 374 / 310 us;
 //   1, 2, 3, 6, 7, 8: 4- and 5-wave tiles with 4 token blocks, and lean
-//     (one MFMA result live) tiles at 4 to 6 waves per SIMD: all slower.
+//     (one MFMA result live) tiles at 5 or 6 waves per SIMD: all slower.
 template <int GROUP, bool ZP>
 static int launch_gr_tile(GemmArgs &a, int sel, hipStream_t st) {
     switch (sel) {
@@ -471,7 +508,8 @@ static int launch_gr_tile(GemmArgs &a, int sel, hipStream_t st) {
     case 6: return launch_gr<2, 5, 1, GROUP, ZP, 2, 5>(a, st);    // 160 rows x 64 tokens, 5 waves, lean
     case 7: return launch_gr<1, 4, 2, GROUP, ZP, 2, 6>(a, st);    // 128 rows x 64 tokens, 8 waves, lean
     case 8: return launch_gr<2, 4, 1, GROUP, ZP, 2, 5>(a, st);    // 128 rows x 64 tokens, 4 waves, lean
-    default: return launch_gr<2, 4, 1, GROUP, ZP, 2, 3>(a, st);   // 128 rows x 64 tokens, 4 waves
+    case 9: return launch_gr<1, 4, 1, GROUP, ZP, 2, 4>(a, st);    // 128 rows x 32 tokens, 4 waves
+    default: return launch_gr<2, 4, 1, GROUP, ZP, 2, 3>(a, st);   // 128 rows x 64 tokens, 4 waves (4)
     }
 }
 
@@ -485,7 +523,13 @@ int launch_gemmr(GemmArgs &a, hipStream_t st) {
         for (int s = 0; s < a.seg_count; ++s)
             if (a.w[i].seg_split[s] != 1) return 1;
     }
-    const int sel = options().gemmr_tile;
+    int sel = options().gemmr_tile;
+    if (sel < 0) {
+        long long tiles = 0;
+        for (int i = 0; i < a.count; ++i) tiles += (a.w[i].M / 16 + 7) / 8;
+        tiles *= (a.T + 63) / 64;
+        sel = tiles >= 3LL * device_cus() ? 4 : 9;
+    }
     const bool zp = a.scale_enc == 1;
     switch (a.group) {
     case 32: return zp ? launch_gr_tile<32, true>(a, sel, st) : launch_gr_tile<32, false>(a, sel, st);

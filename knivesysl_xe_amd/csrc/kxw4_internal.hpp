@@ -130,7 +130,7 @@ struct Options {
     int rowwave_k = 0;                // KXW4_ROWWAVE_K: work-groups per CU, 0 = launcher's plan
     int gemm_kernel = kGemmAuto;      // KXW4_GEMM_KERNEL: auto / general
     int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..9, -1 = cost model
-    int gemmr_tile = -1;              // KXW4_GEMMR_TILE: 0..8, -1 = default
+    int gemmr_tile = -1;              // KXW4_GEMMR_TILE: 0..9, -1 = default
     int w4a4_tile = -1;               // KXW4_W4A4_TILE: 0..4, -1 = default rule
 };
 const Options &options();

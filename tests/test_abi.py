@@ -166,7 +166,7 @@ def test_set_option_checks_names_ranges_and_restores():
             pass
     assert L.kxw4_set_option(b"gemm3_tile", -1, C.byref(prev)) == 0 and prev.value == -1
     assert L.kxw4_set_option(b"w4a4_tile", -1, C.byref(prev)) == 0 and prev.value == -1
-    assert L.kxw4_set_option(b"gemmr_tile", 9, None) == -2
+    assert L.kxw4_set_option(b"gemmr_tile", 10, None) == -2
     with ops.option("gemmr_tile", 8):
         assert L.kxw4_set_option(b"gemmr_tile", 8, C.byref(prev)) == 0 and prev.value == 8
     assert L.kxw4_set_option(b"gemmr_tile", -1, C.byref(prev)) == 0 and prev.value == -1

@@ -550,7 +550,7 @@ def test_gemm3_auto_tile(rows, K, T, group):
     test_gemm3_shapes(rows, K, T, group, None)
 
 
-@pytest.fixture(params=list(range(9)))
+@pytest.fixture(params=list(range(10)))
 def gemmr_tile(request):
     # every tile configuration of the reference-mode large-tile kernel
     with ops.option("gemmr_tile", request.param):
