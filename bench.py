@@ -319,6 +319,55 @@ def measure_refmode(cfg, steps, warmup, eager=False, general=False):
     return res
 
 
+def measure_k16(steps, warmup, eager=False, rows=5120, K=17408, T=1):
+    """The K16 tier (x_gemv_w4a8_core_k16, kernels_dpas.cpp:683-760) on the
+    down projection's shape: seeded int4 codes uniform in [-8, 7], one FP16|zp
+    scale per (row, K16 half) (|N(0,1)| * 0.02, the low nibble a zero point in
+    [-8, 7]), BF16 N(0,1) activations quantized per (token, K32) outside the
+    timed region; the default split plan. HBM-bound: codes + scales stream
+    once per launch."""
+    import torch
+    from knivesysl_xe_amd import ops, workloads
+    from oracle import oracle as O
+    rng = np.random.default_rng(3)
+    codes = rng.integers(-8, 8, (rows, K), dtype=np.int8)
+    mags = (np.abs(rng.standard_normal((rows, K // 16), dtype=np.float32)) * np.float32(0.02))
+    scales = ((mags.astype(np.float16).view(np.uint16) & 0xFFF0)
+              | (rng.integers(-8, 8, (rows, K // 16)) & 0xF)).astype(np.uint16)
+    w = ops.W4Weight.from_codes(torch.from_numpy(codes).cuda(),
+                                torch.from_numpy(scales.view(np.int16)).cuda(), 16, O.SCALE_FP16_ZP4)
+    xb = workloads.f32_to_bf16_bits(rng.standard_normal((T, K), dtype=np.float32))
+    x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+    act = ops.quantize_act(x, 32)
+    out = torch.empty(T, rows, dtype=torch.float32, device="cuda")
+    copies, rot_bytes = make_copies([w])
+    run = lambda ws: ops.gemv(ws[0], act, torch.float32, out=out)
+    secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
+    run(copies[0])
+    torch.cuda.synchronize()
+    q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(xb), 32)
+    ref = O.project(codes, scales, 16, O.SCALE_FP16_ZP4, q, s, sm, 32, O.VAR_GEMV,
+                    O.gemv_splits(rows // 16), rows=(0, 512))
+    exact = bool(np.array_equal(out[:, :512].cpu().numpy().view(np.uint32), ref[:, :512].view(np.uint32)))
+    per = secs / steps
+    nbytes = rows * K // 2 + rows * (K // 16) * 2 + T * K * 2 + T * rows * 4
+    res = {
+        "kernel_us": per * 1e6,
+        "GBps": nbytes / per / 1e9,
+        "TOPS": 2 * T * rows * K / per / 1e12,
+        "bytes": nbytes,
+        "bound": "hbm",
+        "bit_exact_vs_oracle_rows0_512": exact,
+        "rotated_weight_bytes": rot_bytes,
+        "wall_s": wall,
+        "shape": f"T={T}, K={K}, N={rows}, FP16|zp per K16 half (the down projection)",
+    }
+    res["roofline_frac"] = res["GBps"] / HBM_PEAK_GBS
+    del copies, w, out
+    torch.cuda.empty_cache()
+    return res
+
+
 LM_HEAD_ROWS = 248320        # ~1.27 GB of int8 codes at K = 5120 (kernels_dpas.cpp:1576-1577)
 
 
@@ -576,6 +625,7 @@ def main():
     ap.add_argument("--refmode-general", action="store_true",
                     help="also time the reference-mode lines on the general GEMM kernel")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
+    ap.add_argument("--no-k16", action="store_true", help="skip the K16 down-projection GEMV line")
     ap.add_argument("--no-probes", action="store_true", help="skip the MFMA / HBM read probes")
     ap.add_argument("--extra-steps", type=int, default=200,
                     help="timed launches per extra config (each after ~20 ms of warm-up launches)")
@@ -625,6 +675,11 @@ def main():
         log("lm_head_w8a8: W8A8 GEMM, spec wave T=8, K=5120, N=248320 int8")
         e = extra["lm_head_w8a8"] = measure_w8a8(args.extra_steps, 3 if args.eager else None, args.eager)
         log(f"lm_head_w8a8: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, frac {e['roofline_frac']:.3f}, "
+            f"exact={e['bit_exact_vs_oracle_rows0_512']}")
+    if not args.no_k16:
+        log("down_k16: K16 GEMV, T=1, K=17408, N=5120, FP16|zp per K16 half")
+        e = extra["down_k16"] = measure_k16(args.extra_steps, 3 if args.eager else None, args.eager)
+        log(f"down_k16: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, frac {e['roofline_frac']:.3f}, "
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     probes = None
     if not args.no_probes:

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // real tokens and the chain runs on those alone (T = 1: a quarter of the
     // conversions and FMAs)
     constexpr int NR = TT < 4 ? TT : 4;
-    static_assert(TT >= 8 || (WF == kWfW4 && MODE == 0), "short-token chains: per-token W4");
+    static_assert(TT >= 8 || (WF == kWfW4 && MODE == 0) || WF == kWfK16, "short-token chains: per-token W4 and K16");
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
@@ -175,18 +175,23 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
 
     // per-token mode: this lane's four token scales for the output, loaded
     // now (before the ring, so the staging wait below covers them) rather
-    // than after the split sum, where they would add a memory round trip
+    // than after the split sum, where they would add a memory round trip;
+    // likewise the residual of this lane's outputs (one weight per launch).
+    // The K16 instances load them after the stream instead: held across it,
+    // they are the registers its two half MFMAs per unit lack (they spilled).
     float tsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if (a.block == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tsc[r] = a.ascale[min(4 * g4 + r, T - 1)];
-    }
-    // likewise the residual of this lane's outputs (one weight per launch)
     float rsd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.residual) {
+    auto load_epilogue_inputs = [&]() {
+        if (a.block == 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rsd[r] = a.residual[(size_t)min(4 * g4 + r, T - 1) * a.w[0].M + lrow];
-    }
+            for (int r = 0; r < 4; ++r) tsc[r] = a.ascale[min(4 * g4 + r, T - 1)];
+        }
+        if (a.residual) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rsd[r] = a.residual[(size_t)min(4 * g4 + r, T - 1) * a.w[0].M + lrow];
+        }
+    };
+    if constexpr (!K16) load_epilogue_inputs();
 
     // ---- the wave's first split and its ring ----
     const int sb = wj * S / wrg, se = (wj + 1) * S / wrg;
@@ -355,8 +360,12 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     for (int h = 0; h < 2; ++h) {
                                         const float ws = half_bits_to_float((uint16_t)((h ? s1 : s0) & 0xFFF0u));
 #pragma unroll
-                                        for (int r = 0; r < 4; ++r) f0[r] = __builtin_fmaf((float)ph[h][r] * ws, avr[r], f0[r]);
+                                        for (int r = 0; r < NR; ++r) f0[r] = __builtin_fmaf((float)ph[h][r] * ws, avr[r], f0[r]);
                                     }
+                                    // (one unit at a time: hoisting the next units'
+                                    // scale and activation reads above this one's
+                                    // MFMAs made the instance spill)
+                                    __builtin_amdgcn_sched_barrier(0);
                                     continue;
                                 } else if constexpr (W8) {
                                     const v4u hh = ring[p][j >> 1];
@@ -494,6 +503,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // (scalar loads of the kernel arguments, made opaque so the choice stays
     // a select): a per-lane index into the kernel arguments is a vector
     // memory load, whose wait would also wait for the ring's last loads
+    if constexpr (K16) load_epilogue_inputs();
     __attribute__((address_space(1))) uint8_t *wy = (__attribute__((address_space(1))) uint8_t *)a.w[0].y;
     int wm = a.w[0].M;
 #pragma unroll
@@ -657,9 +667,13 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         return alt2 ? rw_ring<16, 32, 1, true, kWfW8>(a, pf, grid, block, lds, st)
                     : rw_ring<16, 32, 1, false, kWfW8>(a, pf, grid, block, lds, st);
     }
-    if (wf == kWfK16)
+    if (wf == kWfK16) {
+        // one or two tokens: the chains of the real tokens' registers only
+        if (a.T == 1) return rw_ring<1, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st);
+        if (a.T == 2) return rw_ring<2, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st);
         return a.T <= 8 ? rw_ring<8, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st)
                         : rw_ring<16, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st);
+    }
     // one or two tokens in per-token mode: the short chains (4-deep ring)
     if (mode == 0 && pf == 4 && a.T == 1) return rw_unit<1>(a, unit, mode, pf, grid, block, lds, st);
     if (mode == 0 && pf == 4 && a.T == 2) return rw_unit<2>(a, unit, mode, pf, grid, block, lds, st);

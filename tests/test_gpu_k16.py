@@ -55,7 +55,8 @@ def test_repack_k16_matches_oracle():
     assert np.array_equal(c.cpu().numpy(), want_codes)
 
 
-@pytest.mark.parametrize("M,K,T", [(64, 384, 1), (1040, 5120, 1), (512, 2048, 8), (256, 1152, 16)])
+@pytest.mark.parametrize("M,K,T", [(64, 384, 1), (1040, 5120, 1), (512, 2048, 8), (256, 1152, 16),
+                                   (256, 1152, 2), (1040, 2048, 3)])
 @pytest.mark.parametrize("splits", [0, 1, 8])
 def test_k16_gemv(M, K, T, splits):
     print(f"k16 gemv M={M} K={K} T={T} splits={splits}", flush=True)
@@ -72,7 +73,7 @@ def test_k16_gemv(M, K, T, splits):
     assert_parity(yr, O.project(codes, scales, 16, 1, q, s, sm, 32, O.VAR_GEMV, S, residual=res), "k16 + res")
 
 
-@pytest.mark.parametrize("M,T", [(1040, 8), (1040, 16), (5120, 16)])
+@pytest.mark.parametrize("M,T", [(1040, 8), (1040, 16), (5120, 16), (5120, 1), (5120, 2)])
 def test_k16_gemv_long_k(M, T):
     # K = 17408 (the down projection): T tokens' activations do not fit in one
     # work-group's LDS with the scale tables, so the launcher runs the tokens
