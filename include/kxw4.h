@@ -106,6 +106,8 @@ const char *kxw4_error_string(int code);
  *   gemm3_tile         -1 cost model, 0..9 one 32x32x32 GEMM tile
  *   gemmr_tile         -1 default, 0..9 one reference-mode (K32 activation
  *                      block) GEMM tile
+ *   gemm3_raster       0 default (4), 1..64 token tiles per XCD raster
+ *                      group of the per-token large-tile GEMM
  *   w4a4_tile          -1 default rule, 0..4 one W4A4 GEMM tile
  * Returns 0, -1 for an unknown name, -2 for a value out of range; *previous
  * (may be NULL) receives the old value. Not synchronised with launches in

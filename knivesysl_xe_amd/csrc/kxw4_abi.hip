@@ -26,6 +26,7 @@ const OptionDesc kOptions[] = {
     {"gemm_kernel", &Options::gemm_kernel, kGemmAuto, kGemmGeneral},
     {"gemm3_tile", &Options::gemm3_tile, -1, 9},
     {"gemmr_tile", &Options::gemmr_tile, -1, 9},
+    {"gemm3_raster", &Options::gemm3_raster, 0, 64},
     {"w4a4_tile", &Options::w4a4_tile, -1, 4},
     {"rowwave_ring", &Options::rowwave_ring, 0, 8},
     {"rowwave_k", &Options::rowwave_k, 0, 64},
@@ -51,6 +52,7 @@ Options from_env() {
         if (!strcmp(e, "general")) o.gemm_kernel = kGemmGeneral;
     num("KXW4_GEMM3_TILE", -1, 9, o.gemm3_tile);
     num("KXW4_GEMMR_TILE", -1, 9, o.gemmr_tile);
+    num("KXW4_GEMM3_RASTER", 0, 64, o.gemm3_raster);
     num("KXW4_W4A4_TILE", -1, 4, o.w4a4_tile);
     return o;
 }

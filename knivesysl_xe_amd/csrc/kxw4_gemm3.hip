@@ -47,7 +47,7 @@
 
 namespace kxw4 {
 
-constexpr int kG3GroupTT = 4;      // token tiles per raster group
+constexpr int kG3GroupTT = 4;      // token tiles per raster group (option gemm3_raster)
 
 #define KXW4_G3_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
@@ -128,10 +128,11 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     const int q8 = nblk / 8, r8 = nblk % 8, xcd = id % 8, j8 = id / 8;
     const int L = xcd < r8 ? xcd * (q8 + 1) + j8 : r8 * (q8 + 1) + (xcd - r8) * q8 + j8;
     const int nnt = a.n_tiles, ntt = a.t_tiles;
-    const int group = L / (kG3GroupTT * nnt);
-    const int first = group * kG3GroupTT;
-    const int gsz = min(ntt - first, kG3GroupTT);
-    const int within = L % (kG3GroupTT * nnt);
+    const int GTT = a.raster_tt;
+    const int group = L / (GTT * nnt);
+    const int first = group * GTT;
+    const int gsz = min(ntt - first, GTT);
+    const int within = L % (GTT * nnt);
     const int tt = first + within % gsz;
     const int ntg = within / gsz;
     int wi = 0;
@@ -603,6 +604,7 @@ static int launch_g3(GemmArgs &a, hipStream_t st) {
     }
     a.n_tiles = nt;
     a.t_tiles = (a.T + S::BM - 1) / S::BM;
+    a.raster_tt = options().gemm3_raster > 0 ? options().gemm3_raster : kG3GroupTT;
     const dim3 grid(a.n_tiles * a.t_tiles), block(S::NTH);
     auto k = gemm3_kernel<TA, TB, WMW, WNW, UNIT, NST, OCC>;
     const size_t lds = (size_t)S::template lds_bytes<NST>();
