@@ -103,7 +103,7 @@ const char *kxw4_error_string(int code);
  *   rowwave_k          row-wave work-groups per CU, 0 = launcher's plan
  *   rowwave_ring       8 = eight weight tiles in flight per wave (else 4)
  *   gemm_kernel        0 auto, 1 the general GEMM for every prefill shape
- *   gemm3_tile         -1 cost model, 0..9 one 32x32x32 GEMM tile
+ *   gemm3_tile         -1 cost model, 0..11 one 32x32x32 GEMM tile
  *   gemmr_tile         -1 default, 0..9 one reference-mode (K32 activation
  *                      block) GEMM tile
  *   gemm3_raster       0 default (4), 1..64 token tiles per XCD raster

@@ -24,7 +24,7 @@ const OptionDesc kOptions[] = {
     {"decode_kernel", &Options::decode_kernel, kDecodeAuto, kDecodeRowwave},
     {"rowwave_spw", &Options::rowwave_spw, 0, 16},
     {"gemm_kernel", &Options::gemm_kernel, kGemmAuto, kGemmGeneral},
-    {"gemm3_tile", &Options::gemm3_tile, -1, 9},
+    {"gemm3_tile", &Options::gemm3_tile, -1, 11},
     {"gemmr_tile", &Options::gemmr_tile, -1, 9},
     {"gemm3_raster", &Options::gemm3_raster, 0, 64},
     {"w4a4_tile", &Options::w4a4_tile, -1, 4},
@@ -50,7 +50,7 @@ Options from_env() {
     num("KXW4_ROWWAVE_K", 0, 64, o.rowwave_k);
     if (const char *e = getenv("KXW4_GEMM_KERNEL"))
         if (!strcmp(e, "general")) o.gemm_kernel = kGemmGeneral;
-    num("KXW4_GEMM3_TILE", -1, 9, o.gemm3_tile);
+    num("KXW4_GEMM3_TILE", -1, 11, o.gemm3_tile);
     num("KXW4_GEMMR_TILE", -1, 9, o.gemmr_tile);
     num("KXW4_GEMM3_RASTER", 0, 64, o.gemm3_raster);
     num("KXW4_W4A4_TILE", -1, 4, o.w4a4_tile);

@@ -55,12 +55,16 @@ constexpr int kG3GroupTT = 4;      // token tiles per raster group (option gemm3
 // format reads zeros), no swizzle, no index.
 constexpr int kBufWord3 = 0x00020000;
 
-template <int TA, int TB, int WMW, int WNW, int UNIT>
+// XB = 1: one more 32-row block column after the waves' own columns, of
+// which each wave takes one 32x32 block (token block wn of its own token
+// range; needs TA == WNW and TB == 1)
+template <int TA, int TB, int WMW, int WNW, int UNIT, int XB = 0>
 struct G3Shape {
     static constexpr int NW = WMW * WNW;
     static constexpr int NTH = 64 * NW;
     static constexpr int BM = WMW * 32 * TA;             // tokens per tile
-    static constexpr int BNG = WNW * 2 * TB;             // row-groups per tile
+    static constexpr int BNG = WNW * 2 * TB + 2 * XB;    // row-groups per tile
+    static_assert(XB == 0 || (XB == 1 && TA == WNW && TB == 1), "extra column: one block per wave");
     static constexpr int UPS = kTileK / UNIT;
     static constexpr int A_BYTES = BM * kTileK;
     static constexpr int B_BYTES = BNG * kTileBytes;
@@ -112,10 +116,10 @@ __device__ __forceinline__ void for_each_index(F &&f, std::integer_sequence<int,
 }
 
 // OCC: waves per SIMD the register budget is sized for
-template <int TA, int TB, int WMW, int WNW, int UNIT, int NST, int OCC>
+template <int TA, int TB, int WMW, int WNW, int UNIT, int NST, int OCC, int XB>
 __global__ __launch_bounds__(64 * WMW * WNW)
 __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs a) {
-    using S = G3Shape<TA, TB, WMW, WNW, UNIT>;
+    using S = G3Shape<TA, TB, WMW, WNW, UNIT, XB>;
     constexpr int NW = S::NW, BM = S::BM, BNG = S::BNG, UPS = S::UPS;
     constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -246,19 +250,27 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     const int jrel0 = wn * 2 * TB + (m32 >> 4);
     const int boff = A_BYTES + jrel0 * kTileBytes + (kg * 16 + (m32 & 15)) * 16;
     const int soff_lds = A_BYTES + B_BYTES + (jrel0 * UPS * 16 + (m32 & 15)) * 2;
+    // extra column (XB): byte distances from this wave's weight and scale
+    // offsets to the extra column's, and the activation offset of its token
+    // block (wave-uniform)
+    const int dxb = (WNW - wn) * 2 * TB * kTileBytes;
+    const int dxs = (WNW - wn) * 2 * TB * UPS * 32;
+    const int dxa = wn * 4096;
     // the same offsets inside the current step's stage, moved on each step
     // (so a read needs no address arithmetic)
     int ast[4], bst = boff, sst = soff_lds;
 #pragma unroll
     for (int c = 0; c < 4; ++c) ast[c] = aoff[c];
 
-    float f[TA][TB][16];
+    float f[TA][TB][16], fx[16];
 #pragma unroll
     for (int i = 0; i < TA; ++i)
 #pragma unroll
         for (int j = 0; j < TB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) f[i][j][r] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) fx[r] = 0.0f;
 
     // Ring of NST stages; step k's loads go to stage k % NST. A wave reaches
     // arrive(k) just before the last 32x32 block of step k - 1 (before the
@@ -311,9 +323,16 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     // chain updates of the block before it (at a step's first block, the
     // previous step's last), so the updates run while the matrix core works.
     // Within a step, token block ib + 1's activations are read at block
-    // (ib, 0) and weight block jb + 1 at block (0, jb), one block ahead.
-    constexpr int NB = TA * TB;
+    // (ib, 0) and weight block jb + 1 at block (0, jb), one block ahead. With
+    // an extra column the step ends with its block: its packed weights and
+    // scales are read two blocks ahead, unpacked and its activations read
+    // one block ahead.
+    constexpr int NBO = TA * TB, NB = NBO + XB;
+    static_assert(XB == 0 || NBO >= 2, "extra column reads two blocks ahead");
     v4i B[TB][4];
+    v4i Bx[4];
+    v4u rawx[2];
+    float wx[UPS];
     v4u raw[2];                        // TB = 1, NB > 1: the next step's packed tile
     v4i Bnext[4];                      // NB = 1: the next step's unpacked tile
     float w[TB][UPS], wnext[TB][UPS], wlast[UPS];
@@ -346,11 +365,18 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
             for (int r = 0; r < 16; ++r)
                 f[ib][jb][r] = __builtin_fmaf((float)p[u][r], wv[u], f[ib][jb][r]);
     };
+    auto update_x = [&](const v16i (&p)[UPS]) {
+#pragma unroll
+        for (int u = 0; u < UPS; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) fx[r] = __builtin_fmaf((float)p[u][r], wx[u], fx[r]);
+    };
     // LDS reads block b issues ahead of its MFMAs
     auto ds_reads = [](int b) {
         const int ib = b / TB, jb = b % TB;
         if (b == NB - 1) return 2 + TB * UPS + 4;
-        return (jb == 0 && ib + 1 < TA ? 4 : 0) + (ib == 0 && jb + 1 < TB ? 2 : 0);
+        return (jb == 0 && ib + 1 < TA ? 4 : 0) + (ib == 0 && jb + 1 < TB ? 2 : 0) +
+               (XB && b == NBO - 2 ? 2 + UPS : 0) + (XB && b == NBO - 1 ? 4 : 0);
     };
     // (the group size must be a literal; the block loop is unrolled, so the
     // switch folds)
@@ -397,6 +423,8 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
     for (int jb = 0; jb < TB; ++jb)
 #pragma unroll
         for (int u = 0; u < UPS; ++u) w[jb][u] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UPS; ++u) wx[u] = 0.0f;
 
     int st = 0;
     // (stc: the step's stage when compile-time, else -1 for the tracked one)
@@ -448,26 +476,44 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
                     read_b(dcur, jb + 1, wd);
                     unpack_b(wd, B[jb + 1]);
                 }
+                if (XB && b == NBO - 2) {
+                    read_b(dcur + dxb, 0, rawx);
+#pragma unroll
+                    for (int u = 0; u < UPS; ++u)
+                        wx[u] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(smem + sst + dcur + dxs + u * 32));
+                }
+                if (XB && b == NBO - 1) {
+                    read_a(dcur + dxa, 0, Anext);
+                    unpack_b(rawx, Bx);
+                }
             }
+            const v4i (&Bo)[4] = b < NBO ? B[jb] : Bx;
             v16i (&p)[UPS] = acc[slot];
             if constexpr (UNIT == 128) {
-                p[0] = mfma32(Acur[0], B[jb][0], zero);
-                p[0] = mfma32(Acur[1], B[jb][1], p[0]);
-                p[0] = mfma32(Acur[2], B[jb][2], p[0]);
-                p[0] = mfma32(Acur[3], B[jb][3], p[0]);
+                p[0] = mfma32(Acur[0], Bo[0], zero);
+                p[0] = mfma32(Acur[1], Bo[1], p[0]);
+                p[0] = mfma32(Acur[2], Bo[2], p[0]);
+                p[0] = mfma32(Acur[3], Bo[3], p[0]);
             } else {
                 static_assert(UNIT == 64, "per-token mode has unit = group in {64, 128}");
-                p[0] = mfma32(Acur[0], B[jb][0], zero);
-                p[UPS - 1] = mfma32(Acur[1], B[jb][1], zero);
-                p[0] = mfma32(Acur[2], B[jb][2], p[0]);
-                p[UPS - 1] = mfma32(Acur[3], B[jb][3], p[UPS - 1]);
+                p[0] = mfma32(Acur[0], Bo[0], zero);
+                p[UPS - 1] = mfma32(Acur[1], Bo[1], zero);
+                p[0] = mfma32(Acur[2], Bo[2], p[0]);
+                p[UPS - 1] = mfma32(Acur[3], Bo[3], p[UPS - 1]);
             }
-            const int ub = b > 0 ? (b - 1) / TB : TA - 1, uj = b > 0 ? (b - 1) % TB : TB - 1;
-            update(ub, uj, acc[slot ^ 1], b > 0 ? w[uj] : wlast);
-            // keep the updates in this block: without a use here the
-            // compiler sinks them past the barrier branch of the last block
+            if (XB && b == 0) {
+                // the previous step's extra block
+                update_x(acc[slot ^ 1]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) asm volatile("" ::"v"(f[ub][uj][r]));
+                for (int r = 0; r < 16; ++r) asm volatile("" ::"v"(fx[r]));
+            } else {
+                const int ub = b > 0 ? (b - 1) / TB : TA - 1, uj = b > 0 ? (b - 1) % TB : TB - 1;
+                update(ub, uj, acc[slot ^ 1], b > 0 ? w[uj] : wlast);
+                // keep the updates in this block: without a use here the
+                // compiler sinks them past the barrier branch of the last block
+#pragma unroll
+                for (int r = 0; r < 16; ++r) asm volatile("" ::"v"(f[ub][uj][r]));
+            }
             // the block's reads, then one MFMA and the VALU share of the
             // previous block's updates, four times
             ds_first(ds_reads(b));
@@ -488,6 +534,11 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
         }
     };
     using Dyn = std::integral_constant<int, -1>;
+    // the last block's updates after the last step
+    auto update_last = [&](const v16i (&p)[UPS]) {
+        if constexpr (XB) update_x(p);
+        else update(TA - 1, TB - 1, p, w[TB - 1]);
+    };
     // after the last step, its last block's updates
     constexpr int LAST0 = (NB - 1) & 1, LAST1 = (2 * NB - 1) & 1;
     if constexpr (kStaticStage) {
@@ -502,11 +553,11 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
         };
         for (; kb + U <= NT; kb += U) for_each_index(one, std::make_integer_sequence<int, U>{});
         for_each_index([&](auto i) { if (kb + decltype(i)::value < NT) one(i); }, std::make_integer_sequence<int, U - 1>{});
-        if (NB % 2 == 1 && ((NT - 1) & 1)) update(TA - 1, TB - 1, acc[LAST1], w[TB - 1]);
-        else update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+        if (NB % 2 == 1 && ((NT - 1) & 1)) update_last(acc[LAST1]);
+        else update_last(acc[LAST0]);
     } else if constexpr (NB % 2 == 0) {
         for (int kb = 0; kb < NT; ++kb) step(kb, std::integral_constant<int, 0>{}, Dyn{});
-        update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+        update_last(acc[LAST0]);
     } else {
         // an odd block count flips the slot parity every step: two steps
         // per iteration keep the slots compile-time
@@ -517,22 +568,76 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
         }
         if (kb < NT) {
             step(kb, std::integral_constant<int, 0>{}, Dyn{});
-            update(TA - 1, TB - 1, acc[LAST0], w[TB - 1]);
+            update_last(acc[LAST0]);
         } else {
-            update(TA - 1, TB - 1, acc[LAST1], w[TB - 1]);
+            update_last(acc[LAST1]);
         }
     }
     // ---- output ----
     // Each wave stages SB token blocks at a time in its own LDS slab (the
     // ring is free once every wave is past its last step) and writes whole
     // 16-byte row runs: register r of block (ib, jb) is token
-    // 8(r/4) + 4kg + r%4 and row m32 of the block.
+    // 8(r/4) + 4kg + r%4 and row m32 of the block. The extra column's block
+    // goes out the same way after the wave's own blocks.
     constexpr int EPS = S::EPS, SB = S::template slab_blocks<NST>();
     static_assert(TA % SB == 0, "slabs cover the wave tile");
     static_assert(S::template lds_bytes<NST>() <= 160 * 1024, "LDS");
     lds_sync();
     float *slab = reinterpret_cast<float *>(smem) + wave * (32 * SB * EPS);
     const float *tsc = reinterpret_cast<const float *>(smem + S::template body_bytes<NST>());
+    // read back runs of CH rows of one token (CH = 8 BF16 or 4 FP32 outputs
+    // = 16 bytes) from NBT token blocks x COLS rows of the slab; tok: the
+    // first token relative to the tile, rgb: the first row-group relative to
+    // the tile. The slab is this wave's own, and its LDS accesses complete in
+    // order
+    auto run = [&](auto ch, auto cols, auto nbt, int tok, int rgb) {
+        constexpr int CH = decltype(ch)::value, COLS = decltype(cols)::value, NBT = decltype(nbt)::value;
+        constexpr int PER_TOKEN = COLS / CH;
+#pragma unroll
+        for (int it = 0; it < 32 * NBT * PER_TOKEN / 64; ++it) {
+            const int q = it * 64 + lane;
+            const int tl = q / PER_TOKEN, rl = (q % PER_TOKEN) * CH;
+            const int t = t0 + tok + tl;
+            const int rg = rg0 + rgb + (rl >> 4);
+            if (t >= T || rg >= RG) continue;
+            const int row = rg * 16 + (rl & 15);
+            const float sc = tsc[tok + tl] * 0.0625f;
+            float v[CH];
+#pragma unroll
+            for (int e = 0; e < CH; e += 4) {
+                const float4 x = *reinterpret_cast<const float4 *>(slab + tl * EPS + rl + e);
+                v[e] = x.x * sc;
+                v[e + 1] = x.y * sc;
+                v[e + 2] = x.z * sc;
+                v[e + 3] = x.w * sc;
+            }
+            if (a.residual) {
+#pragma unroll
+                for (int e = 0; e < CH; e += 4) {
+                    const float4 x = *reinterpret_cast<const float4 *>(a.residual + (size_t)t * M + row + e);
+                    v[e] = v[e] + x.x;
+                    v[e + 1] = v[e + 1] + x.y;
+                    v[e + 2] = v[e + 2] + x.z;
+                    v[e + 3] = v[e + 3] + x.w;
+                }
+            }
+            if constexpr (CH == 8) {
+                uint4 o;
+                o.x = (uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16);
+                o.y = (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16);
+                o.z = (uint32_t)float_to_bf16(v[4]) | ((uint32_t)float_to_bf16(v[5]) << 16);
+                o.w = (uint32_t)float_to_bf16(v[6]) | ((uint32_t)float_to_bf16(v[7]) << 16);
+                *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(W.y) + (size_t)t * M + row) = o;
+            } else {
+                *reinterpret_cast<float4 *>(static_cast<float *>(W.y) + (size_t)t * M + row) =
+                    make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    };
+    auto out_pass = [&](auto cols, auto nbt, int tok, int rgb) {
+        if (a.y_bf16) run(std::integral_constant<int, 8>{}, cols, nbt, tok, rgb);
+        else run(std::integral_constant<int, 4>{}, cols, nbt, tok, rgb);
+    };
 #pragma unroll
     for (int s0 = 0; s0 < TA; s0 += SB) {
 #pragma unroll
@@ -542,61 +647,18 @@ __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm3_kernel(const GemmArgs 
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     slab[(32 * (ib - s0) + 8 * (r >> 2) + 4 * kg + (r & 3)) * EPS + 32 * jb + m32] = f[ib][jb][r];
-        // read back runs of CH rows of one token (CH = 8 BF16 or 4 FP32
-        // outputs = 16 bytes); the slab is this wave's own, and its LDS
-        // accesses complete in order
-        auto run = [&](auto ch) {
-            constexpr int CH = decltype(ch)::value;
-            constexpr int PER_TOKEN = 32 * TB / CH;
+        out_pass(std::integral_constant<int, 32 * TB>{}, std::integral_constant<int, SB>{}, tw + 32 * s0, wn * 2 * TB);
+    }
+    if constexpr (XB) {
 #pragma unroll
-            for (int it = 0; it < 32 * SB * PER_TOKEN / 64; ++it) {
-                const int q = it * 64 + lane;
-                const int tl = q / PER_TOKEN, rl = (q % PER_TOKEN) * CH;
-                const int t = t0 + tw + 32 * s0 + tl;
-                const int rg = rg0 + wn * 2 * TB + (rl >> 4);
-                if (t >= T || rg >= RG) continue;
-                const int row = rg * 16 + (rl & 15);
-                const float sc = tsc[tw + 32 * s0 + tl] * 0.0625f;
-                float v[CH];
-#pragma unroll
-                for (int e = 0; e < CH; e += 4) {
-                    const float4 x = *reinterpret_cast<const float4 *>(slab + tl * EPS + rl + e);
-                    v[e] = x.x * sc;
-                    v[e + 1] = x.y * sc;
-                    v[e + 2] = x.z * sc;
-                    v[e + 3] = x.w * sc;
-                }
-                if (a.residual) {
-#pragma unroll
-                    for (int e = 0; e < CH; e += 4) {
-                        const float4 x = *reinterpret_cast<const float4 *>(a.residual + (size_t)t * M + row + e);
-                        v[e] = v[e] + x.x;
-                        v[e + 1] = v[e + 1] + x.y;
-                        v[e + 2] = v[e + 2] + x.z;
-                        v[e + 3] = v[e + 3] + x.w;
-                    }
-                }
-                if constexpr (CH == 8) {
-                    uint4 o;
-                    o.x = (uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16);
-                    o.y = (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16);
-                    o.z = (uint32_t)float_to_bf16(v[4]) | ((uint32_t)float_to_bf16(v[5]) << 16);
-                    o.w = (uint32_t)float_to_bf16(v[6]) | ((uint32_t)float_to_bf16(v[7]) << 16);
-                    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(W.y) + (size_t)t * M + row) = o;
-                } else {
-                    *reinterpret_cast<float4 *>(static_cast<float *>(W.y) + (size_t)t * M + row) =
-                        make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-        };
-        if (a.y_bf16) run(std::integral_constant<int, 8>{});
-        else run(std::integral_constant<int, 4>{});
+        for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * kg + (r & 3)) * EPS + m32] = fx[r];
+        out_pass(std::integral_constant<int, 32>{}, std::integral_constant<int, 1>{}, tw + 32 * wn, WNW * 2 * TB);
     }
 }
 
-template <int TA, int TB, int WMW, int WNW, int UNIT, int NST, int OCC = 2>
+template <int TA, int TB, int WMW, int WNW, int UNIT, int NST, int OCC = 2, int XB = 0>
 static int launch_g3(GemmArgs &a, hipStream_t st) {
-    using S = G3Shape<TA, TB, WMW, WNW, UNIT>;
+    using S = G3Shape<TA, TB, WMW, WNW, UNIT, XB>;
     int nt = 0;
     for (int i = 0; i < a.count; ++i) {
         a.w[i].nt_begin = nt;
@@ -606,7 +668,7 @@ static int launch_g3(GemmArgs &a, hipStream_t st) {
     a.t_tiles = (a.T + S::BM - 1) / S::BM;
     a.raster_tt = options().gemm3_raster > 0 ? options().gemm3_raster : kG3GroupTT;
     const dim3 grid(a.n_tiles * a.t_tiles), block(S::NTH);
-    auto k = gemm3_kernel<TA, TB, WMW, WNW, UNIT, NST, OCC>;
+    auto k = gemm3_kernel<TA, TB, WMW, WNW, UNIT, NST, OCC, XB>;
     const size_t lds = (size_t)S::template lds_bytes<NST>();
     // the attribute is per device
     static bool attr[64] = {};
@@ -630,6 +692,10 @@ static int launch_g3(GemmArgs &a, hipStream_t st) {
 //   256 x 160 (G128) / 64 x 160 (G64), 10 waves (3 on the busiest SIMD),
 //     one work-group per CU: fits the grid when the 256-row tile leaves
 //     CUs idle;
+//   256 x 160 at G128 as 8 waves of 4 + 1 blocks (each wave's four blocks
+//     of its own 32-row column and one block of the fifth column): 10 blocks
+//     on every SIMD (the waves of a work-group go to the SIMDs in turn, so
+//     ten one-column waves put 12 on two SIMDs and 8 on the others);
 //   128 x 64, 4 waves of 2 blocks, three work-groups per CU;
 //   128 x 256 (G128), 4 waves of 8 blocks, two work-groups per CU: the same
 //     16 blocks per SIMD and step as 256 x 256, but a SIMD's two waves
@@ -642,7 +708,7 @@ static int choose_tile(const GemmArgs &a, int *bm) {
     struct Cand { int sel, bm, bng, wgs, simd_blocks; double penalty; };
     const Cand cands[4] = {
         {0, 256, g128 ? 16 : 8, 1, g128 ? 16 : 8, 1.0},
-        {g128 ? 9 : 8, g128 ? 256 : 64, 10, 1, g128 ? 12 : 3, 1.0},
+        {g128 ? 11 : 8, g128 ? 256 : 64, 10, 1, g128 ? 10 : 3, 1.0},
         {g128 ? 3 : 4, 128, 4, 3, 6, 1.1},
         {1, 128, 16, 2, 16, 0.92},
     };
@@ -676,7 +742,7 @@ int launch_gemm3(GemmArgs &a, hipStream_t st) {
         for (int s = 0; s < a.seg_count; ++s)
             if (a.w[i].seg_split[s] != 1) return 1;
     }
-    // the gemm3_tile option (0..9) picks one configuration (tests, tuning)
+    // the gemm3_tile option (0..11) picks one configuration (tests, tuning)
     const int forced = options().gemm3_tile;
     if (forced >= 0) return launch_tile(a, forced, st);
     int bm = 0;
@@ -688,6 +754,8 @@ static int launch_tile(GemmArgs &a, int sel, hipStream_t st) {
     if (a.group == 128) {
         switch (sel) {
         case 8: return launch_g3<4, 1, 2, 5, 128, 3, 3>(a, st);   // 256 x 160, 10 waves
+        case 10: return launch_g3<4, 1, 2, 4, 128, 3, 2, 1>(a, st);  // 256 x 160, 8 waves of 4 + 1 blocks
+        case 11: return launch_g3<4, 1, 2, 4, 128, 2, 2, 1>(a, st);  // the same, 2 stages
         case 9: return launch_g3<4, 1, 2, 5, 128, 2, 3>(a, st);   // 256 x 160, 10 waves, 2 stages
         case 5: return launch_g3<2, 2, 2, 2, 128, 3, 2>(a, st);   // 128 x 128, 4 waves
         case 6: return launch_g3<2, 2, 1, 4, 128, 3, 2>(a, st);   // 64 x 256, 4 waves

@@ -130,7 +130,7 @@ struct Options {
     int rowwave_ring = 0;             // KXW4_ROWWAVE_RING: weight tiles in flight per wave, 8 (else 4)
     int rowwave_k = 0;                // KXW4_ROWWAVE_K: work-groups per CU, 0 = launcher's plan
     int gemm_kernel = kGemmAuto;      // KXW4_GEMM_KERNEL: auto / general
-    int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..9, -1 = cost model
+    int gemm3_tile = -1;              // KXW4_GEMM3_TILE: 0..11, -1 = cost model
     int gemm3_raster = 0;             // KXW4_GEMM3_RASTER: token tiles per raster group, 0 = 4
     int gemmr_tile = -1;              // KXW4_GEMMR_TILE: 0..9, -1 = default
     int w4a4_tile = -1;               // KXW4_W4A4_TILE: 0..4, -1 = default rule

@@ -156,7 +156,7 @@ def test_set_option_checks_names_ranges_and_restores():
     assert L.kxw4_set_option(b"no_such_option", 0, None) == -1
     assert L.kxw4_set_option(None, 0, None) == -1
     assert L.kxw4_set_option(b"decode_kernel", 3, None) == -2
-    assert L.kxw4_set_option(b"gemm3_tile", 10, None) == -2
+    assert L.kxw4_set_option(b"gemm3_tile", 12, None) == -2
     assert L.kxw4_set_option(b"gemm3_tile", -2, None) == -2
     assert L.kxw4_set_option(b"gemm3_tile", -1, C.byref(prev)) == 0
     assert prev.value == -1

@@ -500,7 +500,7 @@ def gemm_general():
         yield
 
 
-@pytest.fixture(params=list(range(10)))
+@pytest.fixture(params=list(range(12)))
 def gemm3_tile(request):
     # every tile configuration of the large-tile kernel
     with ops.option("gemm3_tile", request.param):
