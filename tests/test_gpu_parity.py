@@ -511,7 +511,7 @@ def gemm3_tile(request):
     # partial token and row tiles, fan-out weights of different heights,
     # fewer K steps than ring stages, both group sizes
     ([1040], 1024, 300, 128), ([1040, 2064], 640, 257, 64), ([4096], 128, 520, 128),
-    ([256], 5120, 2048, 64)])
+    ([256], 5120, 2048, 64), ([1040, 2064], 1024, 520, 128)])
 def test_gemm3_shapes(rows, K, T, group, gemm3_tile):
     rng = np.random.default_rng(sum(rows) + K + T)
     wts = [rand_weight(rng, M, K, group, 0) for M in rows]
