@@ -256,65 +256,85 @@ def measure_w4a4(cfg, steps, warmup, eager=False):
     return res
 
 
-REFMODE_GROUPS = {"cfg3": 32, "cfg2_m512": 64}   # the reference's K32 / K64 weight tiers
+REFMODE_GROUPS = {"cfg3": 32, "cfg2_m512": 64,   # the reference's K32 / K64 weight tiers
+                  "cfg1": 32, "cfg2_m1": 64}
 
 
 def measure_refmode(cfg, steps, warmup, eager=False, general=False):
-    """x_gemm_w4a8 as the reference runs it on a prefill config's shape: the
-    config's codes with FP16|zp scales at the reference's weight group (K32
-    for cfg3, K64 for cfg2 M=512: |N(0,1)| * 0.02 rounded to FP16, the low
-    nibble replaced by a seeded zero point in [-8, 7]), and its BF16
-    activations quantized per (token, K32 block) outside the timed region
-    (x_quantize_act_chunk). general=True times the general GEMM kernel on
-    the same inputs."""
+    """x_gemv_w4a8 / x_gemm_w4a8 as the reference runs them on a config's
+    shape: the config's codes with FP16|zp scales at the reference's weight
+    group (K32 for cfg3 and the cfg1 gate/up pair, K64 for the cfg2 down
+    projection: |N(0,1)| * 0.02 rounded to FP16, the low nibble replaced by
+    a seeded zero point in [-8, 7]), and its BF16 activations quantized per
+    (token, K32 block) outside the timed region (x_quantize_act_chunk).
+    general=True times the general GEMM kernel on the same inputs (GEMM
+    shapes only)."""
     import torch
     from knivesysl_xe_amd import ops, workloads
     from oracle import oracle as O
-    assert len(cfg.rows) == 1 and not cfg.segments
+    assert not cfg.segments
     group = REFMODE_GROUPS[cfg.name]
     inp = workloads.generate(cfg, 0)
     rng = np.random.default_rng(2)
-    N, K, T = cfg.rows[0], cfg.K, cfg.tokens
-    codes = inp.codes[0]
-    mags = (np.abs(rng.standard_normal((N, K // group), dtype=np.float32)) * np.float32(0.02))
-    scales = ((mags.astype(np.float16).view(np.uint16) & 0xFFF0)
-              | (rng.integers(-8, 8, (N, K // group)) & 0xF)).astype(np.uint16)
-    w = ops.W4Weight.from_codes(torch.from_numpy(codes).cuda(),
-                                torch.from_numpy(scales.view(np.int16)).cuda(), group, O.SCALE_FP16_ZP4)
+    K, T = cfg.K, cfg.tokens
+    ws, scs = [], []
+    for codes, N in zip(inp.codes, cfg.rows):
+        mags = (np.abs(rng.standard_normal((N, K // group), dtype=np.float32)) * np.float32(0.02))
+        scales = ((mags.astype(np.float16).view(np.uint16) & 0xFFF0)
+                  | (rng.integers(-8, 8, (N, K // group)) & 0xF)).astype(np.uint16)
+        scs.append(scales)
+        ws.append(ops.W4Weight.from_codes(torch.from_numpy(codes).cuda(),
+                                          torch.from_numpy(scales.view(np.int16)).cuda(), group,
+                                          O.SCALE_FP16_ZP4))
     x = torch.from_numpy(inp.x_bf16.view(np.int16)).cuda().view(torch.bfloat16)
     act = ops.quantize_act(x, 32)
     dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
-    out = torch.empty(T, N, dtype=dt, device="cuda")
-    copies, rot_bytes = make_copies([w])
-    run = lambda ws: ops.gemm(ws[0], act, dt, out=out)
+    outs = [torch.empty(T, N, dtype=dt, device="cuda") for N in cfg.rows]
+    copies, rot_bytes = make_copies(ws)
+    if cfg.kind == "gemv":
+        run = lambda wc: ops.gemv(wc[0], act, dt, out=outs[0])
+    else:
+        run = lambda wc: ops.gemm_fanout(wc, act, dt, outs=outs)
     with ops.option("gemm_kernel", 1 if general else 0):
         secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
         run(copies[0])
     torch.cuda.synchronize()
     q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(inp.x_bf16), 32)
-    sp = O.segment_splits(T, N, K)
-    ref = O.project(codes, scales, group, O.SCALE_FP16_ZP4, q, s, sm, 32, O.VAR_GEMM, sp,
-                    out_bf16=cfg.out_bf16, rows=(0, 512))
-    got = out[:, :512]
-    got = got.view(torch.int16).cpu().numpy().view(np.uint16) if cfg.out_bf16 \
-        else got.cpu().numpy().view(np.uint32)
-    exact = bool(np.array_equal(got, ref[:, :512].view(got.dtype)))
+    exact = True
+    for codes, scales, N, y in zip(inp.codes, scs, cfg.rows, outs):
+        if cfg.kind == "gemv":
+            variant, sp = O.VAR_GEMV, O.gemv_splits(N // 16)
+        else:
+            variant, sp = O.VAR_GEMM, O.segment_splits(T, N, K)
+        ref = O.project(codes, scales, group, O.SCALE_FP16_ZP4, q, s, sm, 32, variant, sp,
+                        out_bf16=cfg.out_bf16, rows=(0, 512))
+        got = y[:, :512]
+        got = got.view(torch.int16).cpu().numpy().view(np.uint16) if cfg.out_bf16 \
+            else got.cpu().numpy().view(np.uint32)
+        exact = exact and bool(np.array_equal(got, ref[:, :512].view(got.dtype)))
     per = secs / steps
+    NS = sum(cfg.rows)
+    hbm = cfg.bound == "hbm"
     res = {
         "kernel_us": per * 1e6,
         "TOPS": cfg.ops() / per / 1e12,
         "ops": cfg.ops(),
-        "bound": "mfma",
+        "bound": cfg.bound,
         "bit_exact_vs_oracle_rows0_512": exact,
         "rotated_weight_bytes": rot_bytes,
-        "bytes": N * K // 2 + N * (K // group) * 2 + T * K + T * (K // 32) * 4 + T * N * 4,
+        # codes, FP16|zp scales, activation input (BF16 for decode, as the
+        # per-token lines count it; int8 codes and K32 scales for prefill)
+        # and output
+        "bytes": NS * K // 2 + NS * (K // group) * 2
+                 + (T * K * 2 if hbm else T * K + T * (K // 32) * 4)
+                 + T * NS * (2 if cfg.out_bf16 else 4),
         "wall_s": wall,
-        "shape": f"T={T}, K={K}, N={N}, FP16|zp group {group}, K32 activation blocks"
-                 + (" (general GEMM kernel)" if general else ""),
+        "shape": f"T={T}, K={K}, N={'+'.join(str(n) for n in cfg.rows)}, FP16|zp group {group}, "
+                 "K32 activation blocks" + (" (general GEMM kernel)" if general else ""),
     }
     res["GBps"] = res["bytes"] / per / 1e9
-    res["roofline_frac"] = res["TOPS"] / INT8_PEAK_TOPS
-    del copies, w, out
+    res["roofline_frac"] = res["GBps"] / HBM_PEAK_GBS if hbm else res["TOPS"] / INT8_PEAK_TOPS
+    del copies, ws, outs
     torch.cuda.empty_cache()
     return res
 
@@ -619,9 +639,9 @@ def main():
                     help="extra BASELINE configs to report ('' for none)")
     ap.add_argument("--w4a4", default="cfg2_m512",
                     help="K64 configs to also run through the W4A4 GEMM ('' for none)")
-    ap.add_argument("--refmode", default="cfg3,cfg2_m512",
-                    help="prefill configs to also run as x_gemm_w4a8 runs them: FP16|zp K32/K64 "
-                         "weights, K32 activation blocks ('' for none)")
+    ap.add_argument("--refmode", default="cfg1,cfg2_m1,cfg3,cfg2_m512",
+                    help="configs to also run as x_gemv_w4a8 / x_gemm_w4a8 run them: FP16|zp "
+                         "K32/K64 weights, K32 activation blocks ('' for none)")
     ap.add_argument("--refmode-general", action="store_true",
                     help="also time the reference-mode lines on the general GEMM kernel")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 lm_head line")
@@ -666,12 +686,13 @@ def main():
             f"exact={e['bit_exact_vs_oracle_rows0_512']}")
     for name in [c for c in args.refmode.split(",") if c]:
         cfg = workloads.CONFIGS[name]
-        for general in ((False, True) if args.refmode_general else (False,)):
+        for general in ((False, True) if args.refmode_general and cfg.kind != "gemv" else (False,)):
             key = f"{name}_ref" + ("_general" if general else "")
-            log(f"{key}: x_gemm_w4a8 on the {name} shape (FP16|zp K{REFMODE_GROUPS[name]} weight, K32 blocks)")
+            fn = "x_gemv_w4a8" if cfg.kind == "gemv" else "x_gemm_w4a8"
+            log(f"{key}: {fn} on the {name} shape (FP16|zp K{REFMODE_GROUPS[name]} weight, K32 blocks)")
             e = extra[key] = measure_refmode(cfg, args.extra_steps, 5 if args.eager else None, args.eager, general)
-            log(f"{key}: {e['kernel_us']:.2f} us, {e['TOPS']:.1f} TOPS, frac {e['roofline_frac']:.3f}, "
-                f"exact={e['bit_exact_vs_oracle_rows0_512']}")
+            log(f"{key}: {e['kernel_us']:.2f} us, {e['GBps']:.1f} GB/s, {e['TOPS']:.1f} TOPS, "
+                f"frac {e['roofline_frac']:.3f}, exact={e['bit_exact_vs_oracle_rows0_512']}")
     if not args.no_w8a8:
         log("lm_head_w8a8: W8A8 GEMM, spec wave T=8, K=5120, N=248320 int8")
         e = extra["lm_head_w8a8"] = measure_w8a8(args.extra_steps, 3 if args.eager else None, args.eager)

@@ -88,8 +88,21 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     static_assert(TT >= 8 || (WF == kWfW4 && MODE == 0) || WF == kWfK16, "short-token chains: per-token W4 and K16");
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
+    // MODE 2 / 3: the reference mode of x_gemv_w4a8 / x_gemm_w4a8 themselves
+    // (K32 activation blocks, FP16|zp weights) with every mode flag known at
+    // compile time (MODE 3: the GEMM's x * (ws * as) association, MODE 2 the
+    // GEMV's and fan-out's (x * ws) * as) and each unit's zero point folded
+    // into the weight bytes (the K16 unpack: bytes w - z), so the MFMA returns
+    // d - z * asum and the code-sum table and its per-output correction are
+    // gone. MODE 1 keeps the other reference-mode combinations (per-token
+    // activations with FP16|zp weights, K32 blocks with plain FP16 weights)
+    // behind runtime flags.
+    constexpr bool ZF = MODE >= 2;
+    static_assert(MODE != 3 || !ALT2, "the GEMM association has one accumulator");
+    static_assert(!ZF || (WF == kWfW4 && UNIT == 32), "folded zero points: W4, K32 units");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
-    constexpr float kInv16 = WF != kWfW4 ? 1.0f : 0.0625f;  // undoes the nibble unpack's factor 16
+    // undoes the nibble unpack's factor 16 (the folded and W8/K16 bytes have none)
+    constexpr float kInv16 = WF != kWfW4 || ZF ? 1.0f : 0.0625f;
     static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -120,22 +133,50 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     const int pitch = K + 16;                                 // padded activation row
     int8_t *Act = reinterpret_cast<int8_t *>(smem);
     uint16_t *Sc = reinterpret_cast<uint16_t *>(smem + (size_t)T * pitch);
+    // The weight that holds a row-group, its first row-group and its
+    // pointers, chosen with uniform indices: scalar loads of the kernel
+    // arguments, made opaque so the choice stays a select. Indexed per lane,
+    // the kernel arguments are vector memory loads, and their wait also
+    // waits for the staging loads issued before them, so the weight ring
+    // would start only once the staging had landed.
+    // (global address space: through the asm statements the compiler could
+    // no longer infer it and would make the ring's loads flat ones)
+    using gcodes_t = __attribute__((address_space(1))) const uint8_t *;
+    using gscales_t = __attribute__((address_space(1))) const uint16_t *;
+    struct WPick { gcodes_t codes; gscales_t scales; int rg_begin, idx; };
+    auto pick_weight = [&](int grp) {
+        WPick w{(gcodes_t)a.w[0].codes, (gscales_t)a.w[0].scales, a.w[0].rg_begin, 0};
+#pragma unroll
+        for (int i = 1; i < kMaxWeights; ++i) {
+            const int j = i < a.count ? i : 0;
+            gcodes_t ci = (gcodes_t)a.w[j].codes;
+            gscales_t si = (gscales_t)a.w[j].scales;
+            int ri = a.w[j].rg_begin;
+            asm volatile("" : "+s"(ci), "+s"(si), "+s"(ri));
+            const bool in = i < a.count && grp >= ri;
+            w.codes = in ? ci : w.codes;
+            w.scales = in ? si : w.scales;
+            w.rg_begin = in ? ri : w.rg_begin;
+            w.idx = in ? i : w.idx;
+        }
+        return w;
+    };
     // the row's weight, its row within the weight, and its pointers
     const int gr = row >> 4;
-    int wsel = 0;
-    for (int i = 1; i < a.count; ++i)
-        if (gr >= a.w[i].rg_begin) wsel = i;
-    const int lrg = gr - a.w[wsel].rg_begin;
+    const WPick wp = pick_weight(gr);
+    const int wsel = wp.idx;
+    const int lrg = gr - wp.rg_begin;
     const int lrow = lrg * 16 + (row & 15);
-    const v4u *wrow = reinterpret_cast<const v4u *>(a.w[wsel].codes + (size_t)lrg * NT * kTileBytes * TB) +
-                      (row & 15) + 16 * g4;
+    __attribute__((address_space(1))) const v4u *wrow =
+        reinterpret_cast<__attribute__((address_space(1))) const v4u *>(wp.codes + (size_t)lrg * NT * kTileBytes * TB) +
+        (row & 15) + 16 * g4;
     const uint16_t *sbase = Sc + (gr - gr_lo) * G * 16 + (row & 15);
-    const uint16_t *wsc = a.w[wsel].scales + ((size_t)lrg * G + g4) * 16 + (row & 15);
+    const gscales_t wsc = wp.scales + ((size_t)lrg * G + g4) * 16 + (row & 15);
 
     // the zero-point code-sum table exists only for FP16|zp W4 weights (W8
     // has no zero points and K16 folds them into the weight bytes), so the
     // other formats ask for less LDS
-    const bool zp = WF == kWfW4 && a.scale_enc == 1;
+    const bool zp = WF == kWfW4 && a.scale_enc == 1 && !ZF;
     // W8 and per-token W4 scales are not staged: they stream through the
     // ring (below)
     float *Asc = reinterpret_cast<float *>(Sc + (W8 || SRW4 ? 0 : a.rw_grmax * G * 16));
@@ -163,10 +204,8 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             } else {
                 const int sx = x - act_chunks, gri = sx / (2 * G), part = sx - gri * 2 * G;
                 const int gr = gr_lo + gri;
-                int wi = 0;
-                for (int i = 1; i < a.count; ++i)
-                    if (gr >= a.w[i].rg_begin) wi = i;
-                src = a.w[wi].scales + (size_t)(gr - a.w[wi].rg_begin) * G * 16 + (size_t)part * 8;
+                const WPick sw = pick_weight(gr);
+                src = (const void *)(sw.scales + (size_t)(gr - sw.rg_begin) * G * 16 + (size_t)part * 8);
             }
             __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(smem + (size_t)c0 * 16),
                                              16, 0, 0);
@@ -207,7 +246,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     uint32_t sring[W8 ? PF : 1];
     // per-token W4: unit j of the tile's scale of this lane's row
     uint16_t wring[SRW4 ? PF : 1][SRW4 ? UPS : 1];
-    const uint16_t *wsr = a.w[wsel].scales + (size_t)lrg * G * 16 + (row & 15);
+    const gscales_t wsr = wp.scales + (size_t)lrg * G * 16 + (row & 15);
     // tile i of the current split; an empty split (more splits than units)
     // or an idle wave reads a valid tile it never uses
     auto load = [&](int i, int p) {
@@ -222,13 +261,24 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
         }
     };
     constexpr int LPT = TB + (W8 ? 1 : 0) + (SRW4 ? UPS : 0);   // loads per tile
+    // With the scales riding in the ring (three loads per tile) the stream
+    // starts after the staging has landed: issued beside it, cfg2 M=1 (17 KB
+    // of activations per work-group) measured 12.4-12.6 against 11.9-12.1 us.
+    if constexpr (SRW4) KXW4_WAIT_VMCNT(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PF; ++p) load(min(p, ntw - 1), p);
     __builtin_amdgcn_sched_barrier(0);
     // the staging loads were issued before the PF ring loads and complete first
     KXW4_WAIT_VMCNT(PF * LPT);
-    const bool ref_block = a.block == 32;
+    // (the epilogue inputs count as arriving here: otherwise the compiler
+    // hoists their first use, the token scale's 1/16, next to their loads,
+    // and the wait it puts there also waits for the staging)
+    if constexpr (!K16) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(tsc[r]), "+v"(rsd[r]));
+    }
+    const bool ref_block = ZF || a.block == 32;
     if (MODE != 0 && UNIT == 32 && ref_block) {
         // per-unit (= per-K32) activation scale and zero-point code sum,
         // [Nu][16 token slots]; each thread reads four consecutive units of
@@ -268,7 +318,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     lds_sync_after_dma();
 
     // ---- streaming: one chain per split, in registers ----
-    const bool gemm_var = a.variant == kVarGemm;
+    const bool gemm_var = ZF ? MODE == 3 : a.variant == kVarGemm;
     // this lane's activation row (MFMA row n; with up to 8 tokens rows 8-15
     // repeat rows 0-7 and are never stored) and its K-slot group
     const int ta = TT <= 8 ? min(n & 7, T - 1) : min(n, T - 1);
@@ -371,6 +421,17 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     const v4u hh = ring[p][j >> 1];
                                     bv = (j & 1) ? (long)(((uint64_t)hh.w << 32) | hh.z)
                                                  : (long)(((uint64_t)hh.y << 32) | hh.x);
+                                } else if constexpr (ZF) {
+                                    // the unit's zero point folded in: nibbles
+                                    // held as w + 8, plus 120 - z per byte, is
+                                    // 128 + w - z in [113, 143] (no carry), and
+                                    // the XOR leaves the int8 bytes w - z
+                                    const uint32_t s0 = *(in ? &sw[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+                                    const uint32_t x = (j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w) ^ 0x88888888u;
+                                    const uint32_t cz = (uint32_t)(120 - sext4(s0)) * 0x01010101u;
+                                    const uint64_t lo = ((x & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
+                                    const uint64_t hi = (((x >> 4) & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
+                                    bv = (long)(lo | (hi << 32));
                                 } else {
                                     bv = unpack_k32(j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w);
                                 }
@@ -393,7 +454,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
 #pragma unroll
                                 for (int r = 0; r < NR; ++r) F[r] = __builtin_fmaf((float)acc[r], ws, F[r]);
                             } else {
-                                const float ws = half_bits_to_float(zp ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
+                                const float ws = half_bits_to_float(zp || ZF ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
                                 const int z = sext4(sv);
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) {
@@ -407,6 +468,16 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     F[r] = nf;
                                 }
                             }
+                        }
+                        // (folded zero points: one unit at a time, its
+                        // chain updates kept in it; with no branch left in
+                        // the unit the compiler otherwise sinks every
+                        // unit's updates below the ring and spills the
+                        // partials)
+                        if constexpr (ZF) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(f0[r]), "+v"(f1[r]));
+                            __builtin_amdgcn_sched_barrier(0);
                         }
                     }
                     if constexpr (LOADS) load(min(i + PF, ntw - 1), p);
@@ -561,6 +632,12 @@ static int rw_mode(const DecodeArgs &a, int mode, int pf, dim3 grid, dim3 block,
     if constexpr (TT < 8) {
         return 1;
     } else {
+        if constexpr (UNIT == 32) {
+            if (mode == 3) return rw_ring<TT, 32, 3, false, kWfW4>(a, pf, grid, block, lds, st);
+            if (mode == 2)
+                return alt2 ? rw_ring<TT, 32, 2, true, kWfW4>(a, pf, grid, block, lds, st)
+                            : rw_ring<TT, 32, 2, false, kWfW4>(a, pf, grid, block, lds, st);
+        }
         return alt2 ? rw_ring<TT, UNIT, 1, true, kWfW4>(a, pf, grid, block, lds, st)
                     : rw_ring<TT, UNIT, 1, false, kWfW4>(a, pf, grid, block, lds, st);
     }
@@ -578,7 +655,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     if (a.T < 1 || a.T > 16) return 1;
     const int unit = a.block == 32 ? 32 : a.group;
     const int nu = a.K / unit, g = a.K / a.group;
-    const int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
+    int mode = (a.block == 0 && a.scale_enc == 0) ? 0 : 1;
     // one split plan for every token and weight
     const int S = a.w[0].seg_split[0];
     if (S < 1 || S > 16 || (S & (S - 1))) return 1;
@@ -590,6 +667,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         rows += a.w[i].M;
     }
     const int wf = a.w8 ? kWfW8 : a.group == 16 ? kWfK16 : kWfW4;
+    // K32 activation blocks against FP16|zp W4 weights (x_gemv_w4a8,
+    // x_gemm_w4a8): the folded-zero-point instances
+    if (wf == kWfW4 && a.block == 32 && a.scale_enc == 1) mode = a.variant == kVarGemm ? 3 : 2;
     if (wf != kWfW4 && (unit != 32 || mode != 1)) return 1;
     if (wf == kWfK16 && a.variant != kVarGemv) return 1;
     const int wrg = std::min(S, kRwSplitWaves);
@@ -621,7 +701,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     // the work-group's LDS: padded activation rows, its row-groups' scales,
     // the per-unit activation scales and, for FP16|zp W4 weights, the
     // zero-point code sums, the split partials, the zero words
-    const bool zp_table = wf == kWfW4 && a.scale_enc == 1;
+    const bool zp_table = wf == kWfW4 && a.scale_enc == 1 && mode < 2;
     auto lds_for = [&](int T) {
         return (size_t)T * (a.K + 16) + (wf == kWfW8 || (wf == kWfW4 && mode == 0 && unit == 64) ? 0 : (size_t)grmax * g * 32) +
                (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) +
