@@ -422,16 +422,20 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     bv = (j & 1) ? (long)(((uint64_t)hh.w << 32) | hh.z)
                                                  : (long)(((uint64_t)hh.y << 32) | hh.x);
                                 } else if constexpr (ZF) {
-                                    // the unit's zero point folded in: nibbles
-                                    // held as w + 8, plus 120 - z per byte, is
-                                    // 128 + w - z in [113, 143] (no carry), and
-                                    // the XOR leaves the int8 bytes w - z
+                                    // the unit's zero point folded in: each
+                                    // nibble w becomes the byte 0x80 | (w ^ 8)
+                                    // = 136 + w (one three-input bit operation),
+                                    // minus z + 8 (the scale word's low nibble
+                                    // XOR 8, broadcast to every byte) leaves
+                                    // 128 + w - z in [113, 143] (no borrow
+                                    // crosses a byte), and the XOR gives the
+                                    // int8 bytes w - z
                                     const uint32_t s0 = *(in ? &sw[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
-                                    const uint32_t x = (j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w) ^ 0x88888888u;
-                                    const uint32_t cz = (uint32_t)(120 - sext4(s0)) * 0x01010101u;
-                                    const uint64_t lo = ((x & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
-                                    const uint64_t hi = (((x >> 4) & 0x0F0F0F0Fu) + cz) ^ 0x80808080u;
-                                    bv = (long)(lo | (hi << 32));
+                                    const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
+                                    const uint32_t zz = __builtin_amdgcn_perm(0u, (s0 & 0xFu) ^ 8u, 0u);
+                                    const uint32_t lo = ((((d ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                                    const uint32_t hi = (((((d >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                                    bv = (long)((uint64_t)lo | ((uint64_t)hi << 32));
                                 } else {
                                     bv = unpack_k32(j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w);
                                 }
