@@ -80,12 +80,12 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // wait (cfg1: 0.7 us slower); group 32 would need four loads per tile
     // and spills.
     constexpr bool SRW4 = WF == kWfW4 && MODE == 0 && UNIT == 64;
-    // TT = 1 or 2 (per-token W4, at most TT tokens): the MFMA leaves token
-    // 4*(l/16) + r in register r of lane l, so only registers r < TT hold
-    // real tokens and the chain runs on those alone (T = 1: a quarter of the
-    // conversions and FMAs)
+    // TT = 1 or 2 (at most TT tokens): the MFMA leaves token 4*(l/16) + r in
+    // register r of lane l, so only registers r < TT hold real tokens and the
+    // chain runs on those alone (T = 1: a quarter of the chain's work)
     constexpr int NR = TT < 4 ? TT : 4;
-    static_assert(TT >= 8 || (WF == kWfW4 && MODE == 0) || WF == kWfK16, "short-token chains: per-token W4 and K16");
+    static_assert(TT >= 8 || (WF == kWfW4 && (MODE == 0 || MODE == 2)) || WF == kWfK16,
+                  "short-token chains: per-token W4, the folded-zero-point GEMV and K16");
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
     // MODE 2 / 3: the reference mode of x_gemv_w4a8 / x_gemm_w4a8 themselves
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                 const float ws = half_bits_to_float(zp || ZF ? (uint16_t)(sv & 0xFFF0u) : (uint16_t)sv);
                                 const int z = sext4(sv);
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) {
+                                for (int r = 0; r < NR; ++r) {
                                     int pv = acc[r];
                                     if (zp) pv -= (z * zv[r]) << 4;
                                     const float pf = (float)pv;
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                         // partials)
                         if constexpr (ZF) {
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(f0[r]), "+v"(f1[r]));
+                            for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(f0[r]), "+v"(f1[r]));
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
@@ -634,6 +634,10 @@ static int rw_mode(const DecodeArgs &a, int mode, int pf, dim3 grid, dim3 block,
         return alt2 ? rw_ring<TT, UNIT, 0, true, kWfW4>(a, pf, grid, block, lds, st)
                     : rw_ring<TT, UNIT, 0, false, kWfW4>(a, pf, grid, block, lds, st);
     if constexpr (TT < 8) {
+        // one or two tokens: the folded-zero-point GEMV only
+        if constexpr (UNIT == 32) {
+            if (mode == 2 && alt2) return rw_ring<TT, 32, 2, true, kWfW4>(a, pf, grid, block, lds, st);
+        }
         return 1;
     } else {
         if constexpr (UNIT == 32) {
@@ -758,9 +762,11 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
         return a.T <= 8 ? rw_ring<8, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st)
                         : rw_ring<16, 32, 1, true, kWfK16>(a, 4, grid, block, lds, st);
     }
-    // one or two tokens in per-token mode: the short chains (4-deep ring)
-    if (mode == 0 && pf == 4 && a.T == 1) return rw_unit<1>(a, unit, mode, pf, grid, block, lds, st);
-    if (mode == 0 && pf == 4 && a.T == 2) return rw_unit<2>(a, unit, mode, pf, grid, block, lds, st);
+    // one or two tokens in per-token mode or the folded-zero-point GEMV: the
+    // short chains (4-deep ring)
+    const bool short_ok = pf == 4 && (mode == 0 || (mode == 2 && a.variant == kVarGemv));
+    if (short_ok && a.T == 1) return rw_unit<1>(a, unit, mode, pf, grid, block, lds, st);
+    if (short_ok && a.T == 2) return rw_unit<2>(a, unit, mode, pf, grid, block, lds, st);
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf, grid, block, lds, st);
     return rw_unit<16>(a, unit, mode, pf, grid, block, lds, st);
 }

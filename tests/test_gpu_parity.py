@@ -660,7 +660,9 @@ def test_packed_equals_serial(M, segments):
     (4096, 4096, 1, 32, 32, 1), (5120, 17408, 1, 64, 32, 1), (512, 1024, 4, 64, 32, 1),
     (64, 512, 2, 128, 0, 0), (48, 256, 1, 32, 32, 1), (16, 128, 1, 32, 32, 1),
     (256, 2048, 50, 32, 32, 1), (128, 17408, 20, 64, 32, 1), (2048, 2048, 13, 64, 32, 1),
-    (1024, 4096, 5, 128, 0, 0), (64, 512, 16, 64, 0, 0)])
+    (1024, 4096, 5, 128, 0, 0), (64, 512, 16, 64, 0, 0),
+    # two tokens on the reference arithmetic (the two-token instance)
+    (1024, 2048, 2, 32, 32, 1), (528, 4096, 2, 64, 32, 1)])
 def test_gemv_reference_mode(M, K, T, group, block, enc):
     rng = np.random.default_rng(M * 3 + K)
     codes, scales = rand_weight(rng, M, K, group, enc)
