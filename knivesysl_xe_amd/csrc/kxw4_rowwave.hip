@@ -361,6 +361,24 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
 #pragma unroll
                         for (int j = 0; j < 4; ++j) s8[j] = (uint32_t)__shfl((int)sring[p], n + 16 * j);
                     }
+                    // folded zero points with one or two tokens: the tile's
+                    // scale words and activation scales, read together
+                    // before its units (read per unit, each unit waited
+                    // for its own two LDS round trips)
+                    constexpr bool kTileScales = ZF && NR < 4;
+                    uint32_t zsw[kTileScales ? UPS : 1];
+                    float zas[kTileScales ? UPS : 1][NR];
+                    if constexpr (kTileScales) {
+#pragma unroll
+                        for (int j = 0; j < UPS; ++j) {
+                            const int u = kb * UPS + j;
+                            const bool in = !PRED || (i < ntw && (u >= u0 && u < u1));
+                            zsw[j] = *(in ? &sbase[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+                            const float *ap = in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4;
+#pragma unroll
+                            for (int r = 0; r < NR; ++r) zas[j][r] = ap[r];
+                        }
+                    }
 #pragma unroll
                     for (int j = 0; j < UPS; ++j) {
                         const int u = kb * UPS + j;
@@ -374,7 +392,10 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                         }
                         float avr[4] = {1.0f, 1.0f, 1.0f, 1.0f};
                         v4i zv = {0, 0, 0, 0};
-                        if constexpr (MODE != 0) {
+                        if constexpr (kTileScales) {
+#pragma unroll
+                            for (int r = 0; r < NR; ++r) avr[r] = zas[j][r];
+                        } else if constexpr (MODE != 0) {
                             const float4 a4 = *reinterpret_cast<const float4 *>(in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4);
                             avr[0] = a4.x;
                             avr[1] = a4.y;
@@ -430,7 +451,9 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     // 128 + w - z in [113, 143] (no borrow
                                     // crosses a byte), and the XOR gives the
                                     // int8 bytes w - z
-                                    const uint32_t s0 = *(in ? &sw[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+                                    uint32_t s0;
+                                    if constexpr (kTileScales) s0 = zsw[j];
+                                    else s0 = *(in ? &sw[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
                                     const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
                                     const uint32_t zz = __builtin_amdgcn_perm(0u, (s0 & 0xFu) ^ 8u, 0u);
                                     const uint32_t lo = ((((d ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
@@ -446,6 +469,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                             uint32_t sv;
                             if constexpr (W8) sv = in ? s8[j] : 0u;
                             else if constexpr (SRW4) sv = in ? (uint32_t)wring[p][j] : 0u;
+                            else if constexpr (kTileScales) sv = zsw[j];
                             else sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
                             // GEMV: units at odd offsets from the split start feed the
                             // second accumulator. With an even ring and an even number
@@ -477,11 +501,14 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                         // chain updates kept in it; with no branch left in
                         // the unit the compiler otherwise sinks every
                         // unit's updates below the ring and spills the
-                        // partials)
+                        // partials. With one or two tokens the registers
+                        // allow the units of a tile to overlap: their LDS
+                        // reads issue together and each chain update runs
+                        // after the next unit's MFMA.)
                         if constexpr (ZF) {
 #pragma unroll
                             for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(f0[r]), "+v"(f1[r]));
-                            __builtin_amdgcn_sched_barrier(0);
+                            if constexpr (NR >= 4) __builtin_amdgcn_sched_barrier(0);
                         }
                     }
                     if constexpr (LOADS) load(min(i + PF, ntw - 1), p);
