@@ -77,11 +77,15 @@ def launcher(cfg, act, outs):
 WARM_MS = 20.0      # warm-up GPU time before a timed region (the shader clock's ramp)
 
 
-def time_graph(run, copies, steps, warmup):
+def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
     """Capture `steps` launches in one graph, replay it between syncs. With
     warmup=None the warm-up graph holds about WARM_MS of launches, sized from
     a replay of 10 (the clock ramps up over the first milliseconds of load, so
-    a fixed small count under-warms short kernels)."""
+    a fixed small count under-warms short kernels). settle_ms > 0 runs about
+    that much GPU time of untimed launches of the same kernel right before the
+    `warmup` launches (their count goes to info["settle_launches"]), so that
+    a short explicit warm-up does not start the timed launches on a clock
+    that is still ramping."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -113,6 +117,20 @@ def time_graph(run, copies, steps, warmup):
     gw = capture(max(warmup, 1), 0)
     gt = capture(steps, max(warmup, 1))
     torch.cuda.synchronize()
+    if settle_ms > 0:
+        g10 = capture(10, 0)
+        g10.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g10.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        reps = int(min(max(settle_ms / max(e0.elapsed_time(e1), 1e-3), 1), 2000))
+        for _ in range(reps):
+            g10.replay()
+        if info is not None:
+            info["settle_launches"] = 10 * (reps + 2)
     gw.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -165,14 +183,18 @@ def time_eager(run, copies, steps, warmup):
     return e0.elapsed_time(e1) / 1e3, time.perf_counter() - t0
 
 
-def measure(cfg, steps, warmup, eager=False):
+def measure(cfg, steps, warmup, eager=False, settle_ms=0.0):
     import torch
     inp, ws, x, act = setup(cfg)
     dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
     outs = [torch.empty(cfg.tokens, w.M, dtype=dt, device="cuda") for w in ws]
     run = launcher(cfg, act, outs)
     copies, rot_bytes = make_copies(ws)
-    secs, wall = (time_eager if eager else time_graph)(run, copies, steps, warmup)
+    info = {}
+    if eager:
+        secs, wall = time_eager(run, copies, steps, warmup)
+    else:
+        secs, wall = time_graph(run, copies, steps, warmup, settle_ms, info)
     run(copies[0])
     torch.cuda.synchronize()
     exact = check_against_oracle(cfg, inp, outs)
@@ -196,6 +218,8 @@ def measure(cfg, steps, warmup, eager=False):
         "quantize_us": quant_us,
         "wall_s": wall,
     }
+    if "settle_launches" in info:
+        res["settle_launches"] = info["settle_launches"]
     res["roofline_frac"] = (res["GBps"] / HBM_PEAK_GBS if cfg.bound == "hbm"
                             else res["TOPS"] / INT8_PEAK_TOPS)
     del copies, ws, outs
@@ -712,7 +736,12 @@ def main():
             f"{probes['hbm_read_headline_bytes_GBps']:.0f} GB/s (headline bytes); ns per block per SIMD: "
             + ", ".join(f"{k[6:-13]} {v:.1f}" for k, v in probes.items() if k.startswith("issue_") and k.endswith("_ns_per_block")))
     log(f"headline {head.note}")
-    r = measure(head, args.steps, args.warmup, args.eager)
+    # Before its `warmup` launches the headline kernel also runs ~WARM_MS of
+    # untimed launches, as every other line does: after the driver's 5
+    # warm-up launches alone its 20 timed launches read 19.5-19.9 us, with
+    # the settle pass 19.2-19.4 us; 1000 timed launches read ~18.5 us (a
+    # replay carries a fixed ~14 us that 20 launches share).
+    r = measure(head, args.steps, args.warmup, args.eager, settle_ms=WARM_MS)
     log(f"cfg1: {r['kernel_us']:.2f} us/launch, {r['GBps']:.1f} GB/s, exact={r['bit_exact_vs_oracle_rows0_512']}")
     if args.copy_mib:
         calibration_copy(args.copy_mib)
@@ -727,6 +756,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_launches": r.get("settle_launches"),
         "ms_per_step": round(per * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
