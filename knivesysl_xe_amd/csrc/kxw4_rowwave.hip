@@ -365,15 +365,21 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                     // scale words and activation scales, read together
                     // before its units (read per unit, each unit waited
                     // for its own two LDS round trips)
-                    constexpr bool kTileScales = ZF && NR < 4;
-                    uint32_t zsw[kTileScales ? UPS : 1];
+                    // (K16 with one or two tokens likewise: its units' two
+                    // scale words each)
+                    constexpr bool kTileScales = (ZF || K16) && NR < 4;
+                    constexpr int SWU = K16 ? 2 : 1;              // scale words per unit
+                    uint32_t zsw[kTileScales ? UPS : 1][SWU];
                     float zas[kTileScales ? UPS : 1][NR];
                     if constexpr (kTileScales) {
 #pragma unroll
                         for (int j = 0; j < UPS; ++j) {
                             const int u = kb * UPS + j;
                             const bool in = !PRED || (i < ntw && (u >= u0 && u < u1));
-                            zsw[j] = *(in ? &sbase[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
+#pragma unroll
+                            for (int q = 0; q < SWU; ++q)
+                                zsw[j][q] = *(in ? &sbase[(K16 ? 2 * u + q : (u >> gsh)) * 16]
+                                                 : reinterpret_cast<const uint16_t *>(Zero) + n);
                             const float *ap = in ? Asc + u * 16 + 4 * g4 : Zero + 4 * g4;
 #pragma unroll
                             for (int r = 0; r < NR; ++r) zas[j][r] = ap[r];
@@ -416,7 +422,32 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                              : mfma_k64(A1, unpack_k64(wd.z, wd.w), zero);
                             } else {
                                 long bv;
-                                if constexpr (K16) {
+                                if constexpr (K16 && kTileScales) {
+                                    // the unit's two K16 scale words (lane groups
+                                    // 0-1 carry half 0, 2-3 half 1), its zero point
+                                    // folded in as in the folded-zero-point
+                                    // instances: bytes 0x80 | (w ^ 8) minus z + 8,
+                                    // then XOR 0x80 (the bytes w - z)
+                                    const uint32_t s0 = zsw[j][0], s1 = zsw[j][1];
+                                    const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
+                                    const uint32_t zz = __builtin_amdgcn_perm(0u, ((g4 < 2 ? s0 : s1) & 0xFu) ^ 8u, 0u);
+                                    const uint32_t lo = ((((d ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                                    const uint32_t hi = (((((d >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                                    bv = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                                    const v4i ph[2] = {mfma_k32(av, g4 < 2 ? bv : 0l, zero), mfma_k32(av, g4 < 2 ? 0l : bv, zero)};
+#pragma unroll
+                                    for (int h = 0; h < 2; ++h) {
+                                        const float ws = half_bits_to_float((uint16_t)((h ? s1 : s0) & 0xFFF0u));
+#pragma unroll
+                                        for (int r = 0; r < NR; ++r) f0[r] = __builtin_fmaf((float)ph[h][r] * ws, zas[j][r], f0[r]);
+                                    }
+                                    // (with one or two tokens the registers allow a
+                                    // tile's units to overlap; the chain updates stay
+                                    // in unit order)
+#pragma unroll
+                                    for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(f0[r]));
+                                    continue;
+                                } else if constexpr (K16) {
                                     // the unit's two K16 scale words; lane groups
                                     // 0-1 carry half 0, 2-3 half 1
                                     const uint32_t s0 = *(in ? &sw[(2 * u) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
@@ -452,7 +483,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     // crosses a byte), and the XOR gives the
                                     // int8 bytes w - z
                                     uint32_t s0;
-                                    if constexpr (kTileScales) s0 = zsw[j];
+                                    if constexpr (kTileScales) s0 = zsw[j][0];
                                     else s0 = *(in ? &sw[(u >> gsh) * 16] : reinterpret_cast<const uint16_t *>(Zero) + n);
                                     const uint32_t d = j == 0 ? wd.x : j == 1 ? wd.y : j == 2 ? wd.z : wd.w;
                                     const uint32_t zz = __builtin_amdgcn_perm(0u, (s0 & 0xFu) ^ 8u, 0u);
@@ -469,7 +500,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                             uint32_t sv;
                             if constexpr (W8) sv = in ? s8[j] : 0u;
                             else if constexpr (SRW4) sv = in ? (uint32_t)wring[p][j] : 0u;
-                            else if constexpr (kTileScales) sv = zsw[j];
+                            else if constexpr (kTileScales) sv = zsw[j][0];
                             else sv = *(in ? sp : reinterpret_cast<const uint16_t *>(Zero) + n);
                             // GEMV: units at odd offsets from the split start feed the
                             // second accumulator. With an even ring and an even number
