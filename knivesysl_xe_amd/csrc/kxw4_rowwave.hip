@@ -84,7 +84,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // register r of lane l, so only registers r < TT hold real tokens and the
     // chain runs on those alone (T = 1: a quarter of the chain's work)
     constexpr int NR = TT < 4 ? TT : 4;
-    static_assert(TT >= 8 || (WF == kWfW4 && (MODE == 0 || MODE == 2)) || WF == kWfK16,
+    static_assert(TT >= 8 || (WF == kWfW4 && (MODE == 0 || MODE == 2 || MODE == 4)) || WF == kWfK16,
                   "short-token chains: per-token W4, the folded-zero-point GEMV and K16");
     static_assert(WF == kWfW4 || (UNIT == 32 && MODE == 1), "W8 / K16: K32 units, reference mode");
     static_assert(!K16 || ALT2, "K16 is a GEMV");
@@ -96,9 +96,12 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // d - z * asum and the code-sum table and its per-output correction are
     // gone. MODE 1 keeps the other reference-mode combinations (per-token
     // activations with FP16|zp weights, K32 blocks with plain FP16 weights)
-    // behind runtime flags.
+    // behind runtime flags. MODE 4 / 5 are MODE 2 / 3 at weight group 64 as
+    // a compile-time fact, so the two units of a group share their scale
+    // word's zero-point broadcast and scale conversion.
     constexpr bool ZF = MODE >= 2;
-    static_assert(MODE != 3 || !ALT2, "the GEMM association has one accumulator");
+    constexpr bool ZGEMM = MODE == 3 || MODE == 5;
+    static_assert(!ZGEMM || !ALT2, "the GEMM association has one accumulator");
     static_assert(!ZF || (WF == kWfW4 && UNIT == 32), "folded zero points: W4, K32 units");
     constexpr int TB = W8 ? 2 : 1;                 // 16-byte loads per lane and tile
     // undoes the nibble unpack's factor 16 (the folded and W8/K16 bytes have none)
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     const int S = a.rw_S, wrg = a.rw_wrg, spw = a.rw_spw;
     const int K = a.K, T = a.T;
     const int NT = K / kTileK, Nu = K / UNIT, G = K / a.group;
-    const int gsh = a.group >= UNIT ? __builtin_ctz(a.group / UNIT) : 0;
+    const int gsh = MODE >= 4 ? 1 : a.group >= UNIT ? __builtin_ctz(a.group / UNIT) : 0;
 
     // ---- this work-group's halves [h0, h1), this wave's slice ----
     const int b = blockIdx.x, NWG = gridDim.x, H = a.rw_halves;
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     lds_sync_after_dma();
 
     // ---- streaming: one chain per split, in registers ----
-    const bool gemm_var = ZF ? MODE == 3 : a.variant == kVarGemm;
+    const bool gemm_var = ZF ? ZGEMM : a.variant == kVarGemm;
     // this lane's activation row (MFMA row n; with up to 8 tokens rows 8-15
     // repeat rows 0-7 and are never stored) and its K-slot group
     const int ta = TT <= 8 ? min(n & 7, T - 1) : min(n, T - 1);
@@ -695,14 +698,19 @@ static int rw_mode(const DecodeArgs &a, int mode, int pf, dim3 grid, dim3 block,
         // one or two tokens: the folded-zero-point GEMV only
         if constexpr (UNIT == 32) {
             if (mode == 2 && alt2) return rw_ring<TT, 32, 2, true, kWfW4>(a, pf, grid, block, lds, st);
+            if (mode == 4 && alt2) return rw_ring<TT, 32, 4, true, kWfW4>(a, pf, grid, block, lds, st);
         }
         return 1;
     } else {
         if constexpr (UNIT == 32) {
             if (mode == 3) return rw_ring<TT, 32, 3, false, kWfW4>(a, pf, grid, block, lds, st);
+            if (mode == 5) return rw_ring<TT, 32, 5, false, kWfW4>(a, pf, grid, block, lds, st);
             if (mode == 2)
                 return alt2 ? rw_ring<TT, 32, 2, true, kWfW4>(a, pf, grid, block, lds, st)
                             : rw_ring<TT, 32, 2, false, kWfW4>(a, pf, grid, block, lds, st);
+            if (mode == 4)
+                return alt2 ? rw_ring<TT, 32, 4, true, kWfW4>(a, pf, grid, block, lds, st)
+                            : rw_ring<TT, 32, 4, false, kWfW4>(a, pf, grid, block, lds, st);
         }
         return alt2 ? rw_ring<TT, UNIT, 1, true, kWfW4>(a, pf, grid, block, lds, st)
                     : rw_ring<TT, UNIT, 1, false, kWfW4>(a, pf, grid, block, lds, st);
@@ -735,7 +743,9 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     const int wf = a.w8 ? kWfW8 : a.group == 16 ? kWfK16 : kWfW4;
     // K32 activation blocks against FP16|zp W4 weights (x_gemv_w4a8,
     // x_gemm_w4a8): the folded-zero-point instances
-    if (wf == kWfW4 && a.block == 32 && a.scale_enc == 1) mode = a.variant == kVarGemm ? 3 : 2;
+    // (modes 4 / 5: the same at group 64)
+    if (wf == kWfW4 && a.block == 32 && a.scale_enc == 1)
+        mode = (a.variant == kVarGemm ? 3 : 2) + (a.group == 64 ? 2 : 0);
     if (wf != kWfW4 && (unit != 32 || mode != 1)) return 1;
     if (wf == kWfK16 && a.variant != kVarGemv) return 1;
     const int wrg = std::min(S, kRwSplitWaves);
@@ -822,7 +832,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     }
     // one or two tokens in per-token mode or the folded-zero-point GEMV: the
     // short chains (4-deep ring)
-    const bool short_ok = pf == 4 && (mode == 0 || (mode == 2 && a.variant == kVarGemv));
+    const bool short_ok = pf == 4 && (mode == 0 || ((mode == 2 || mode == 4) && a.variant == kVarGemv));
     if (short_ok && a.T == 1) return rw_unit<1>(a, unit, mode, pf, grid, block, lds, st);
     if (short_ok && a.T == 2) return rw_unit<2>(a, unit, mode, pf, grid, block, lds, st);
     if (a.T <= 8) return rw_unit<8>(a, unit, mode, pf, grid, block, lds, st);
