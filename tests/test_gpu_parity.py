@@ -701,7 +701,9 @@ def test_gemv_fanout(rows, T, block, enc, group):
     (17408 // 4, 5120, 8, 32, 1, 32, 0), (5120, 5120, 24, 32, 1, 64, 0), (1024, 2048, 128, 32, 1, 32, 0),
     (5120, 5120, 8, 0, 0, 128, 16), (768, 4096, 200, 0, 0, 64, 0), (512, 2048, 40, 0, 0, 128, 0),
     (1024, 4096, 64, 32, 1, 32, 0), (256, 17408, 61, 0, 0, 64, 0), (4096, 5120, 16, 0, 0, 128, 0),
-    (1024, 4096, 12, 32, 1, 32, 0), (2048, 2048, 5, 32, 1, 64, 4), (512, 1024, 3, 0, 0, 64, 8)])
+    (1024, 4096, 12, 32, 1, 32, 0), (2048, 2048, 5, 32, 1, 64, 4), (512, 1024, 3, 0, 0, 64, 8),
+    # the group-64 folded-zero-point decode GEMM at 8 and 16 tokens
+    (2048, 4096, 8, 32, 1, 64, 0), (1040, 2048, 12, 32, 1, 64, 0)])
 def test_gemm_modes(M, K, T, block, enc, group, forced):
     rng = np.random.default_rng(M + T)
     codes, scales = rand_weight(rng, M, K, group, enc)
