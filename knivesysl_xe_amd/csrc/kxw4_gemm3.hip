@@ -4,11 +4,15 @@
 // token.
 //
 // Cost model (measured on the MI355X): the FP32 chain needs one int->float
-// conversion and one FMA per output and weight group, as many VALU cycles as
-// the MFMA cycles of a 16x16x64 product over a 128-K group. A 16x16x64 int8
-// MFMA leaves the VALU about one free issue slot, so with it the two simply
-// add up; a 32x32x32 int8 MFMA (twice the work, twice the cycles) leaves
-// about five, so most of the chain runs under the matrix core. Hence:
+// conversion and one FMA per output and weight group. A 32x32 block's four
+// 32x32x32 MFMAs over a 128-K step take ~131 cycles of the matrix core and
+// its 32 chain instructions per lane ~70 cycles of the VALU, and a SIMD
+// overlaps the two only partly: interleaved in one wave they take the sum
+// (~217 cycles), in two or four waves per SIMD ~190 and ~174. Per 32x32
+// block the 16x16x64 MFMA is 13-18% slower still (it needs twice the operand
+// bytes per MAC and leaves fewer issue slots). The kernel is therefore
+// bound by issuing the chain beside the MFMAs, and it is laid out to keep
+// both busy and to add little else:
 //   * each wave owns a 32*TA token x 32*TB row tile of 32x32 blocks; a block
 //     is four dependent MFMAs over a 128-K step followed by its 16 chain
 //     updates per lane, and the scheduler overlaps one block's updates with
