@@ -27,12 +27,14 @@
 //
 // The activations (T x K int8) and the work-group's FP16 scales are staged
 // into LDS once per work-group with direct global->LDS loads, so the
-// weight-tile loads are the only vector-memory instructions of the streaming
-// loop. Activation rows are padded by 16 bytes, so the 8 or 16 token rows a
-// 16-lane quarter reads fall on distinct banks. Whole rings run without
-// predicates; only a split's last, partial ring selects the old accumulator
-// for its padded positions. Weight tiles are read once per launch, so their
-// loads are non-temporal (they do not displace the activations from L2).
+// weight-tile loads (and, for the per-token group-64 and W8 instances, the
+// scales that ride beside them) are the only vector-memory instructions of
+// the streaming loop. Activation rows are padded by 16 bytes, so the 8 or 16
+// token rows a 16-lane quarter reads fall on distinct banks. Whole rings run
+// without predicates; only a split's last, partial ring selects the old
+// accumulator for its padded positions. Weight tiles are read once per
+// launch, so their loads are non-temporal (they do not displace the
+// activations from L2).
 //
 // W8 (the W8A8 tier, x_gemv_w8a8_core / x_gemm_w8a8, kernels_dpas.cpp:
 // 771-844, 1578-1629): 2 KB int8 tiles, two 16-byte loads per lane and tile,
