@@ -353,7 +353,7 @@ static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
     // quantize_blk_kernel; 16-byte vector loads and stores of the rows and
     // 8-byte code stores, so the rows must start on 16 bytes. With few
     // tokens a row's work-group is most of the launch, so it takes 1024
-    // threads (more loads in flight per row; T=1, K=17408: 6.3 -> ~3 us);
+    // threads (more loads in flight per row; T=1, K=17408: 6.3 -> 4.5 us);
     // RMSNorm keeps 256 for its fixed-order row sum.
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
     const int nch = a.K / 8;
