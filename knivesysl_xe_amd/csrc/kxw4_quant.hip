@@ -1,5 +1,6 @@
 // kxw4_quant.hip — activation quantizers (kernels_dpas.cpp:188-223, 846-929,
-// 1149-1207), one work-group per token row.
+// 1149-1207): rows spread over work-groups when few, else one work-group per
+// row.
 //
 // A producer computes the fp32 value of element k (plain load, SiLU(g)*u, or
 // (1+w) RMSNorm); the quantizer turns it into int8 with
@@ -7,12 +8,17 @@
 //   q = clamp(rint(v / s), -127, 127)          (IEEE division, NaN -> -127)
 // over blocks of 32 K (reference mode) or the whole row (per-token mode), and
 // writes exact int32 code sums per K32. Codes are stored in the MFMA slot
-// order of each 64-element chunk (act_slot).
+// order of each 64-element chunk (act_slot). The chunk kernels divide once
+// per chunk or row and multiply by the reciprocal, taking the division only
+// where that could round differently (rint_quot), so their codes are the
+// division's.
 //
-// Block 32: the 32 lanes of a half wave hold one block, so absmax and sums are
-// half-wave shuffles and each element is produced once. Per-token: a first pass
-// reduces the row absmax across the work-group, a second pass quantizes
-// (producers are recomputed, bit-identically).
+// The element-loop fallback (rows not on 16 bytes, or per-token rows longer
+// than the chunk kernels hold): in block 32 the 32 lanes of a half wave hold
+// one block, so absmax and sums are half-wave shuffles and each element is
+// produced once; per-token, a first pass reduces the row absmax across the
+// work-group, a second pass quantizes (producers are recomputed,
+// bit-identically).
 #include "kxw4_device.hpp"
 #include "kxw4_internal.hpp"
 
@@ -90,6 +96,50 @@ __device__ __forceinline__ int8_t quantize_one(float v, float s) {
     return (int8_t)(int)clampf(rintf(v / s), -127.0f, 127.0f);
 }
 
+// rint(v / s) of N values, bit for bit, without a division per value:
+// y = v * r with r the hardware reciprocal of s (within 1 ulp of 1/s; the
+// bound below allows 2). Where |v| <= m and s is m / L rounded (the block or
+// row absmax over the code limit L), |v / s| <= L (1 + 2^-23) and y differs
+// from the rounded quotient fl(v / s) by at most |v / s| * 1.5 * 2^-22,
+// 4.6e-5 at L = 127; so where y lies further than 2^-14 from every half-integer,
+// fl(v / s) lies on the same side of it and both round to the same integer.
+// The other values (about one in 8,000 for smooth data), and every value when
+// s < 2^-120 (whose reciprocal could overflow), take the division itself. A
+// NaN value gives NaN on both paths; an infinite one makes s infinite, r 0
+// and y NaN as v / s is, and every finite value of its block 0 on both.
+template <int N>
+__device__ __forceinline__ void rint_quot(const float (&v)[N], float s, float (&k)[N]) {
+    const float r = __builtin_amdgcn_rcpf(s);
+    float d = 0.0f;   // largest distance of a y from its integer (NaN y: none)
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const float y = v[j] * r;
+        k[j] = rintf(y);
+        d = fmaxf(d, fabsf(y - k[j]));
+    }
+    if (!(s >= 0x1p-120f) || d > 0.5f - 0x1p-14f) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) k[j] = rintf(v[j] / s);
+    }
+}
+
+// The int8 codes of a chunk of 8 values at scale s, as quantize_one gives
+// them, packed in element order, and their sum (two signed byte dot products
+// with ones).
+__device__ __forceinline__ uint2 quantize_chunk(const float (&v)[8], float s, int &sum) {
+    float k[8];
+    rint_quot(v, s, k);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int8_t q = (int8_t)(int)clampf(k[j], -127.0f, 127.0f);
+        if (j < 4) lo |= (uint32_t)(uint8_t)q << (8 * j);
+        else hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
+    }
+    sum = __builtin_amdgcn_sdot4((int)hi, 0x01010101, __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false), false);
+    return make_uint2(lo, hi);
+}
+
 // The element loops below take kQU elements per thread and pass: all kQU
 // loads are issued (at indices clamped into the row) before any is used, so a
 // pass costs one memory round trip instead of one per element; the values of
@@ -99,17 +149,20 @@ constexpr int kQU = 8;
 
 // 1 / sqrt(mean(x^2) + eps) of row t, summed in a fixed order: thread tid
 // adds x[k]^2 for k = tid, tid + kQThreads, ... in turn, then the work-group
-// sum (the work-group must have kQThreads threads)
+// sum (the work-group must have kQThreads threads). The loads go 32 to a
+// memory round trip (H = 17408: three round trips instead of nine); the
+// adds keep their order.
 __device__ __forceinline__ float row_rms_inv(const QuantArgs &a, int t, float *red) {
+    constexpr int B = 32;
     const int K = a.K, tid = threadIdx.x;
     const float *row = static_cast<const float *>(a.x) + (size_t)t * K;
     float ss = 0.0f;
-    for (int k0 = tid; k0 < K; k0 += kQThreads * kQU) {
-        float x[kQU];
+    for (int k0 = tid; k0 < K; k0 += kQThreads * B) {
+        float x[B];
 #pragma unroll
-        for (int u = 0; u < kQU; ++u) x[u] = row[min(k0 + u * kQThreads, K - 1)];
+        for (int u = 0; u < B; ++u) x[u] = row[min(k0 + u * kQThreads, K - 1)];
 #pragma unroll
-        for (int u = 0; u < kQU; ++u)
+        for (int u = 0; u < B; ++u)
             if (k0 + u * kQThreads < K) ss += x[u] * x[u];
     }
     ss = block_reduce_sum(ss, red);
@@ -172,18 +225,19 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantArgs a) {
 }
 
 // The values of this thread's NCH chunks of 8 consecutive elements of row t
-// (chunk tid + c*NT), every chunk's inputs loaded before any is used, at
-// chunk indices clamped into the row (a chunk past the row holds the last
+// (chunk first + tid + c*NT), every chunk's inputs loaded before any is used,
+// at chunk indices clamped into the row (a chunk past the row holds the last
 // chunk's values and is not used); the per-element arithmetic is produce's.
 template <int P, int NCH, int NT>
-__device__ __forceinline__ void chunk_values(const QuantArgs &a, int t, float rms_inv, float (&v)[NCH][8]) {
+__device__ __forceinline__ void chunk_values(const QuantArgs &a, int t, float rms_inv, float (&v)[NCH][8],
+                                             int first = 0) {
     const int nch = a.K / 8, tid = threadIdx.x;
     const size_t row0 = (size_t)t * a.K;
     uint4 raw[NCH][P == kLoadBF16 || P == kRmsNorm ? 1 : 2];
     float4 upv[P == kSiluMul ? NCH : 1][2];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int idx = min(tid + c * NT, nch - 1);
+        const int idx = min(first + tid + c * NT, nch - 1);
         if constexpr (P == kLoadBF16) {
             raw[c][0] = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + row0)[idx];
         } else {
@@ -232,14 +286,15 @@ __device__ __forceinline__ void store_chunk_out(const QuantArgs &a, int t, int i
     o[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// Per-token mode with plain loads, one pass: each thread holds chunks of 8
-// consecutive elements (16-byte bf16 / 32-byte f32 loads) in registers for the
-// whole row, so the row is read once. The MFMA slot order keeps the 8 codes of
-// a chunk contiguous: chunk c of 64-element chunk h lands at byte
+// One row per work-group: each thread holds chunks of 8 consecutive
+// elements (16-byte bf16 / 32-byte f32 loads) in registers for the whole
+// row, so the row is read once. The MFMA slot order keeps the 8 codes of a
+// chunk contiguous: chunk c of 64-element chunk h lands at byte
 // 64h + 16(c & 3) + 8((c >> 2) & 1), one 8-byte store. The four chunks of a
-// K32 block sit in four consecutive lanes, so their code sum is a 4-lane
-// shuffle.
-template <int P, int NCH, int NT = kQThreads>
+// K32 block sit in four consecutive lanes, so a block's absmax (K32 mode)
+// and code sum are 4-lane shuffles; the per-token absmax is a work-group
+// reduction.
+template <int P, int NCH, int NT = kQThreads, bool PER_TOKEN = true>
 __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
     static_assert(P != kRmsNorm || NT == kQThreads, "the row sum's order assumes kQThreads threads");
     __shared__ float red[NT / 64];
@@ -249,139 +304,192 @@ __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
     if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
     float v[NCH][8];
     chunk_values<P, NCH, NT>(a, t, rms_inv, v);
-    float mx = -INFINITY;
+    float s = 1.0f;
+    if constexpr (PER_TOKEN) {
+        float mx = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        if (tid + c * NT < nch) {
-            if (P >= kSiluMul && a.out) store_chunk_out<NCH>(a, t, tid + c * NT, v[c]);
+        for (int c = 0; c < NCH; ++c) {
+            if (tid + c * NT < nch) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+            }
         }
+        // work-group max (order-free, so any thread count gives the same bits)
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        mx = red[0];
+#pragma unroll
+        for (int i = 1; i < NT / 64; ++i) mx = fmaxf(mx, red[i]);
+        s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+        if (tid == 0) a.scale[t] = s;
     }
-    // work-group max (order-free, so any thread count gives the same bits)
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = red[0];
-#pragma unroll
-    for (int i = 1; i < NT / 64; ++i) mx = fmaxf(mx, red[i]);
-    const float s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
-    if (tid == 0) a.scale[t] = s;
     int8_t *qrow = a.q + (size_t)t * K;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int idx = tid + c * NT;
         // whole K32 blocks (4 chunks) per 4-lane group: nch % 4 == 0
         if (idx - (tid & 3) < nch) {
-            uint32_t lo = 0, hi = 0;
-            int sum = 0;
-            if (idx < nch) {
+            const bool in = idx < nch;
+            if (P >= kSiluMul && a.out && in) store_chunk_out<NCH>(a, t, idx, v[c]);
+            if constexpr (!PER_TOKEN) {
+                float mx = fabsf(v[c][0]);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int8_t q = quantize_one(v[c][j], s);
-                    sum += q;
-                    if (j < 4) lo |= (uint32_t)(uint8_t)q << (8 * j);
-                    else hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
-                }
-                *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
-                    make_uint2(lo, hi);
+                for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+                mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+                s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
             }
+            int sum = 0;
+            const uint2 codes = quantize_chunk(v[c], s, sum);
+            if (in) *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) = codes;
             sum += __shfl_xor(sum, 1, 64);
             sum += __shfl_xor(sum, 2, 64);
-            if (a.sum && (idx & 3) == 0 && idx < nch) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
+            if (in && (idx & 3) == 0) {
+                if (!PER_TOKEN) a.scale[(size_t)t * (K / 32) + (idx >> 2)] = s;
+                if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
+            }
         }
     }
 }
 
-// Reference mode (K32 blocks) in one pass: each thread holds chunks of 8
-// consecutive elements, so a K32 block is 4 consecutive lanes and its absmax
-// and code sum are two lane shuffles each (one element per lane would take
-// five dependent shuffles per reduction and element). Every chunk's inputs
-// are loaded before any is used, at chunk indices clamped into the row; the
-// per-element arithmetic is the element loop's (produce), and the codes of a
-// chunk are one 8-byte store in the slot order. RMSNorm keeps kQThreads
-// threads for its fixed-order row sum.
-template <int P, int NCH, int NT = kQThreads>
-__global__ __launch_bounds__(NT) void quantize_blk_kernel(QuantArgs a) {
-    static_assert(P != kRmsNorm || NT == kQThreads, "the row sum's order assumes kQThreads threads");
+// Rows spread over work-groups: work-group b = t*G + g quantizes chunks
+// [g*NT, (g+1)*NT) of row t (G = ceil(nch / NT)), one chunk per thread, so
+// with few tokens a row's quantization runs on G CUs instead of one. K32
+// blocks (4 chunks, 4 consecutive lanes) need only their own chunk: absmax
+// and code sum are two lane shuffles each. A per-token scale needs the row's
+// absmax, so each work-group of a row produces the whole row as the per-row
+// kernel does (NCH chunks per thread, G <= NCH) and reduces it -- a max per
+// element, against the quantization it leaves to the chunk's owner -- and
+// keeps its own chunk, c = g, in registers. RMSNorm's row sum is likewise
+// computed by every work-group of the row in the per-row kernel's order, so
+// every work-group sees the same bits.
+template <int P, int NCH, bool PER_TOKEN>
+__global__ __launch_bounds__(kQThreads) void quantize_spread_kernel(QuantArgs a, int G) {
+    static_assert(PER_TOKEN || NCH == 1, "K32 blocks: one chunk per thread");
     __shared__ float red[kQThreads / 64];
-    const int t = blockIdx.x, K = a.K, tid = threadIdx.x;
-    const int nch = K / 8;
+    const int t = blockIdx.x / G, g = blockIdx.x - t * G;
+    const int K = a.K, tid = threadIdx.x, nch = K / 8;
+    const int idx = g * kQThreads + tid;
+    const bool in = idx < nch;   // a K32 block's four chunks are all in the row or all past it
     float rms_inv = 0.0f;
     if constexpr (P == kRmsNorm) rms_inv = row_rms_inv(a, t, red);
-    const size_t row0 = (size_t)t * K;
-    float v[NCH][8];
-    chunk_values<P, NCH, NT>(a, t, rms_inv, v);
-    int8_t *qrow = a.q + row0;
+    float w[8];
+    float s;
+    if constexpr (PER_TOKEN) {
+        float v[NCH][8];
+        chunk_values<P, NCH, kQThreads>(a, t, rms_inv, v);
+        float mx = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int idx = tid + c * NT;
-        // a K32 block's four chunks are all in the row or all past it
-        const bool in = idx < nch;
-        if (a.out && in) store_chunk_out<NCH>(a, t, idx, v[c]);
-        float mx = fabsf(v[c][0]);
+        for (int c = 0; c < NCH; ++c) {
+            if (tid + c * kQThreads < nch) {
 #pragma unroll
-        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        mx = red[0];
+#pragma unroll
+        for (int i = 1; i < kQThreads / 64; ++i) mx = fmaxf(mx, red[i]);
+        s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+        if (g == 0 && tid == 0) a.scale[t] = s;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            if (c == g) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) w[j] = v[c][j];
+            }
+        }
+    } else {
+        float v[1][8];
+        chunk_values<P, 1, kQThreads>(a, t, rms_inv, v, g * kQThreads);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = v[0][j];
+        float mx = fabsf(w[0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(w[j]));
         mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-        const float sc = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
-        uint32_t lo = 0, hi = 0;
-        int sum = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int8_t q = quantize_one(v[c][j], sc);
-            sum += q;
-            if (j < 4) lo |= (uint32_t)(uint8_t)q << (8 * j);
-            else hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
-        }
-        if (in) *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
-                    make_uint2(lo, hi);
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        if (in && (idx & 3) == 0) {
-            a.scale[(size_t)t * (K / 32) + (idx >> 2)] = sc;
-            if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
-        }
+        s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
+    }
+    if (P >= kSiluMul && a.out && in) store_chunk_out<1>(a, t, idx, w);
+    int sum = 0;
+    const uint2 codes = quantize_chunk(w, s, sum);
+    if (in)
+        *reinterpret_cast<uint2 *>(a.q + (size_t)t * K + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
+            codes;
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (in && (idx & 3) == 0) {
+        if (!PER_TOKEN) a.scale[(size_t)t * (K / 32) + (idx >> 2)] = s;
+        if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
     }
 }
 
 template <int P>
 static int launch_q(const QuantArgs &a, int block, hipStream_t st) {
-    // One pass with the row's chunks in registers, up to 20480 elements:
-    // per-token (block 0) on quantize_tok_kernel, K32 blocks on
-    // quantize_blk_kernel; 16-byte vector loads and stores of the rows and
-    // 8-byte code stores, so the rows must start on 16 bytes. With few
-    // tokens a row's work-group is most of the launch, so it takes 1024
-    // threads (more loads in flight per row; T=1, K=17408: 6.3 -> 4.5 us);
-    // RMSNorm keeps 256 for its fixed-order row sum.
+    // One pass with the chunks in registers: 16-byte vector loads and stores
+    // of the rows and 8-byte code stores, so the rows must start on 16 bytes.
+    // K32 blocks: rows spread over work-groups, one chunk per thread (RMSNorm
+    // with many rows: one work-group per row, up to 20480 elements).
+    // Per-token: spread as well while one work-group per row would leave CUs
+    // idle (T below the CU count) and every work-group can hold its row (at
+    // most 12 chunks per thread, K <= 24576), else one work-group per row (up
+    // to 20480 elements; T=1, K=17408: 4.5 us on one 1024-thread work-group
+    // before the rows were spread, 3.3 us spread).
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
     const int nch = a.K / 8;
-    if (a.K % 32 == 0 && al(a.x, 16) && al(a.up, 16) && al(a.w, 16) && al(a.out, 16) && al(a.q, 8)) {
-        auto run = [&](auto kernel1024_1, auto kernel1024_3, auto kernel2, auto kernel4, auto kernel10) {
-            if (P != kRmsNorm && a.T < 64 && nch <= 3 * 1024) {
-                if (nch <= 1024) hipLaunchKernelGGL(kernel1024_1, dim3(a.T), dim3(1024), 0, st, a);
-                else hipLaunchKernelGGL(kernel1024_3, dim3(a.T), dim3(1024), 0, st, a);
-                return true;
-            }
-            if (nch > 10 * kQThreads) return false;
-            if (nch <= 2 * kQThreads) hipLaunchKernelGGL(kernel2, dim3(a.T), dim3(kQThreads), 0, st, a);
-            else if (nch <= 4 * kQThreads) hipLaunchKernelGGL(kernel4, dim3(a.T), dim3(kQThreads), 0, st, a);
-            else hipLaunchKernelGGL(kernel10, dim3(a.T), dim3(kQThreads), 0, st, a);
-            return true;
+    const int G = (nch + kQThreads - 1) / kQThreads;   // work-groups per spread row
+    if (a.K % 32 == 0 && al(a.x, 16) && al(a.up, 16) && al(a.w, 16) && al(a.out, 16) && al(a.q, 8) &&
+        (long long)a.T * G < (1ll << 31)) {
+        auto spread = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)(a.T * G)), dim3(kQThreads), 0, st, a, G);
+            return hipGetLastError() == hipSuccess ? 0 : -6;
         };
-        // (RMSNorm has no 1024-thread instances: the null pointers are never launched)
-        constexpr bool k1024 = P != kRmsNorm;
-        bool done;
-        if (block == 32)
-            done = run(k1024 ? quantize_blk_kernel<P, 1, k1024 ? 1024 : kQThreads> : nullptr,
-                       k1024 ? quantize_blk_kernel<P, 3, k1024 ? 1024 : kQThreads> : nullptr,
-                       quantize_blk_kernel<P, 2>, quantize_blk_kernel<P, 4>, quantize_blk_kernel<P, 10>);
-        else
-            done = run(k1024 ? quantize_tok_kernel<P, 1, k1024 ? 1024 : kQThreads> : nullptr,
-                       k1024 ? quantize_tok_kernel<P, 3, k1024 ? 1024 : kQThreads> : nullptr,
-                       quantize_tok_kernel<P, 2>, quantize_tok_kernel<P, 4>, quantize_tok_kernel<P, 10>);
-        if (done) return hipGetLastError() == hipSuccess ? 0 : -6;
+        auto per_row = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(a.T), dim3(kQThreads), 0, st, a);
+            return hipGetLastError() == hipSuccess ? 0 : -6;
+        };
+        const int cus = device_cus();
+        if (block == 32) {
+            // RMSNorm's row sum is computed by every work-group of a spread
+            // row: with many rows, once per row instead (T=512, H=17408:
+            // 50 us spread)
+            if (P != kRmsNorm || a.T < cus) return spread(quantize_spread_kernel<P, 1, false>);
+            if constexpr (P == kRmsNorm) {
+                if (nch <= 2 * kQThreads) return per_row(quantize_tok_kernel<P, 2, kQThreads, false>);
+                if (nch <= 3 * kQThreads) return per_row(quantize_tok_kernel<P, 3, kQThreads, false>);
+                if (nch <= 4 * kQThreads) return per_row(quantize_tok_kernel<P, 4, kQThreads, false>);
+                if (nch <= 10 * kQThreads) return per_row(quantize_tok_kernel<P, 10, kQThreads, false>);
+            }
+        } else {
+            if (a.T < cus && G <= 12) {
+                if (G <= 1) return spread(quantize_spread_kernel<P, 1, true>);
+                if (G <= 2) return spread(quantize_spread_kernel<P, 2, true>);
+                if (G <= 3) return spread(quantize_spread_kernel<P, 3, true>);
+                if (G <= 5) return spread(quantize_spread_kernel<P, 5, true>);
+                if (G <= 9) return spread(quantize_spread_kernel<P, 9, true>);
+                return spread(quantize_spread_kernel<P, 12, true>);
+            }
+            // rows past 16384 elements: 1024 threads per row fill the CUs'
+            // wave slots at a few hundred rows (T=512, K=17408: 7.9 against
+            // 8.7 us); shorter rows would leave a third of those threads idle
+            // (T=2048, K=5120: 13.3 against 9.5 us)
+            if constexpr (P != kRmsNorm) {
+                if (nch > 2048 && nch <= 3072) {
+                    hipLaunchKernelGGL((quantize_tok_kernel<P, 3, 1024>), dim3(a.T), dim3(1024), 0, st, a);
+                    return hipGetLastError() == hipSuccess ? 0 : -6;
+                }
+            }
+            if (nch <= 2 * kQThreads) return per_row(quantize_tok_kernel<P, 2>);
+            if (nch <= 3 * kQThreads) return per_row(quantize_tok_kernel<P, 3>);
+            if (nch <= 4 * kQThreads) return per_row(quantize_tok_kernel<P, 4>);
+            if (nch <= 10 * kQThreads) return per_row(quantize_tok_kernel<P, 10>);
+        }
     }
     if (block == 32)
         hipLaunchKernelGGL((quantize_kernel<P, false>), dim3(a.T), dim3(kQThreads), 0, st, a);
@@ -434,11 +542,13 @@ __global__ __launch_bounds__(256) void quantize_s4_kernel(const void *x, int T, 
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
     const float s = (mx > 0.0f) ? (mx / 7.0f) : 1.0f;
+    float k[8];
+    rint_quot(v, s, k);
     uint32_t w = 0;
     int sm = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int q = (int)clampf(rintf(v[j] / s), -7.0f, 7.0f);
+        const int q = (int)clampf(k[j], -7.0f, 7.0f);
         sm += q;
         w |= (uint32_t)(q & 0xF) << (j < 4 ? 8 * j : 8 * (j - 4) + 4);
     }

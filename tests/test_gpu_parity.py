@@ -15,7 +15,7 @@ torch = pytest.importorskip("torch")
 
 from knivesysl_xe_amd import ops, workloads  # noqa: E402
 from oracle import oracle as O  # noqa: E402
-from tests.test_oracle import gemm_check_input, random_payload  # noqa: E402
+from tests.test_oracle import gemm_check_input, random_payload, rounding_boundary_rows  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -137,10 +137,11 @@ def test_quantizer_golden(golden, mode, block):
     assert np.array_equal(a.sum.cpu().numpy(), golden[key + "_sum"])
 
 
+@pytest.mark.parametrize("T,K", [(7, 5120), (260, 5120), (260, 17408)])
 @pytest.mark.parametrize("block", [32, 0])
-def test_quantizer_bf16_input(block):
+def test_quantizer_bf16_input(T, K, block):
     rng = np.random.default_rng(3)
-    xb = workloads.f32_to_bf16_bits(rng.standard_normal((7, 5120)).astype(np.float32) * 3)
+    xb = workloads.f32_to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32) * 3)
     a = ops.quantize_act(dev(xb.view(np.int16)).view(torch.bfloat16), block)
     q, s, sm = O.quantize_act(workloads.bf16_bits_to_f32(xb), block)
     assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
@@ -149,9 +150,8 @@ def test_quantizer_bf16_input(block):
 
 
 @pytest.mark.parametrize("T,K", [
-    # every launch shape of the K32-block quantizer: 1024 threads with one or
-    # three chunks per thread (few tokens), 256 threads with 2, 4 or 10, and
-    # rows past 10 chunks per thread (the element loop)
+    # the K32-block quantizer spreads rows over ceil(K/2048) work-groups at
+    # any T: one to twelve work-groups per row, few and many rows
     (1, 4096), (2, 17408), (70, 4096), (64, 8192), (65, 20480), (64, 24576)])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_quantizer_block_shapes(T, K, bf16):
@@ -165,6 +165,31 @@ def test_quantizer_block_shapes(T, K, bf16):
     else:
         a = ops.quantize_act(dev(x), 32)
     q, s, sm = O.quantize_act(x, 32)
+    assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm)
+
+
+@pytest.mark.parametrize("T,K,block", [
+    # K32 blocks (rows spread over 2, 9 and 1 work-groups), per-token rows
+    # spread over 1, 2, 3, 4, 9 and 12 work-groups (the 1, 2, 3, 5, 9 and 12
+    # chunk instances), and per-token rows of one work-group each (T at
+    # least the CU count: 2, 3, 4 and 10 chunks of 256 threads, 3 of 1024)
+    (1, 4096, 32), (3, 17408, 32), (300, 1024, 32),
+    (7, 640, 0), (1, 4096, 0), (3, 5120, 0), (4, 8192, 0), (2, 17408, 0), (5, 24576, 0),
+    (300, 2048, 0), (260, 5120, 0), (260, 8192, 0), (260, 12288, 0), (260, 17408, 0)])
+def test_quantizer_rounding_boundaries(T, K, block):
+    # values at and within 3 ulp of every rounding boundary of v / s, scales
+    # from subnormal to 2^114, and a NaN and an infinity: the quantizers'
+    # reciprocal products must give the division's codes everywhere
+    print(f"quant boundaries T={T} K={K} block={block}", flush=True)
+    rng = np.random.default_rng(T * 13 + K + block)
+    x = rounding_boundary_rows(rng, T, K, 32 if block else K, 127)
+    x[0, 37] = np.nan
+    if T > 1:
+        x[T - 1, 70] = np.inf
+    a = ops.quantize_act(dev(x), block)
+    q, s, sm = O.quantize_act(x, block)
     assert np.array_equal(ops.act_codes_natural(a).cpu().numpy(), q)
     assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.view(np.uint32))
     assert np.array_equal(a.sum.cpu().numpy(), sm)
@@ -186,11 +211,11 @@ def test_quantizer_block_unaligned_rows():
     assert np.array_equal(a.sum.cpu().numpy(), sm)
 
 
-@pytest.mark.parametrize("T,K", [(70, 4096), (1, 5120), (64, 20480)])
+@pytest.mark.parametrize("T,K", [(70, 4096), (1, 5120), (64, 20480), (300, 1024)])
 @pytest.mark.parametrize("block", [32, 0])
 def test_silu_mul_quant_shapes(T, K, block):
-    # the SiLU quantizers at 256 and 1024 threads per row and 2 to 10 chunks
-    # per thread
+    # the SiLU quantizers with rows spread over 2, 3 and 10 work-groups, and
+    # per-token rows of one work-group each
     rng = np.random.default_rng(T + K)
     gate = (rng.uniform(-1, 1, (T, K)) * 8).astype(np.float32)
     up = (rng.uniform(-1, 1, (T, K)) * 4).astype(np.float32)
@@ -243,10 +268,13 @@ def test_rmsnorm_quant(block):
     assert np.array_equal(a.sum.cpu().numpy(), sm)
 
 
-@pytest.mark.parametrize("T,H", [(70, 4096), (2, 17408), (1, 512)])
+@pytest.mark.parametrize("T,H", [(70, 4096), (2, 17408), (1, 512), (300, 640), (260, 5120),
+                                 (260, 17408)])
 @pytest.mark.parametrize("block", [32, 0])
 def test_rmsnorm_quant_shapes(T, H, block):
-    # the RMSNorm quantizers at 2, 4 and 10 chunks per thread
+    # the RMSNorm quantizers with rows spread over 2, 9 and 1 work-groups, and
+    # rows of one work-group each (T at least the CU count: 2, 3 and 10
+    # chunks per thread)
     rng = np.random.default_rng(T * 3 + H)
     x = rng.standard_normal((T, H)).astype(np.float32)
     w = O.f32_to_bf16(rng.standard_normal(H).astype(np.float32) * 0.1)

@@ -10,7 +10,7 @@ torch = pytest.importorskip("torch")
 
 from knivesysl_xe_amd import ops  # noqa: E402
 from oracle import oracle as O  # noqa: E402
-from tests.test_oracle import gemm_check_input  # noqa: E402
+from tests.test_oracle import gemm_check_input, rounding_boundary_rows  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -77,6 +77,20 @@ def test_s4_quantizer(T, K, dtype):
     q, s, sm = O.quantize_act_s4(x)
     torch.cuda.synchronize()
     assert np.array_equal(a.q4.cpu().numpy().reshape(-1), s4_layout_bytes(q, T, K))
+    assert np.array_equal(ops.s4_codes_natural(a).cpu().numpy(), q)
+    assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.T.copy().view(np.uint32))
+    assert np.array_equal(a.sum.cpu().numpy(), sm.T)
+
+
+@pytest.mark.parametrize("T,K", [(1, 4096), (37, 1024)])
+def test_s4_quantizer_rounding_boundaries(T, K):
+    # values at and within 3 ulp of every rounding boundary of v / s per K64
+    # block: the reciprocal products must give the division's codes
+    rng = np.random.default_rng(T + K)
+    x = rounding_boundary_rows(rng, T, K, 64, 7)
+    a = ops.quantize_act_s4(dev(x))
+    q, s, sm = O.quantize_act_s4(x)
+    torch.cuda.synchronize()
     assert np.array_equal(ops.s4_codes_natural(a).cpu().numpy(), q)
     assert np.array_equal(a.scale.cpu().numpy().view(np.uint32), s.T.copy().view(np.uint32))
     assert np.array_equal(a.sum.cpu().numpy(), sm.T)

@@ -194,6 +194,48 @@ def test_quantizer_divides_rather_than_multiplies_by_reciprocal():
     pytest.skip("no distinguishing case found")
 
 
+def rounding_boundary_rows(rng, T, K, group, limit):
+    """x[T][K] fp32 whose groups of `group` values (a K32 block, a K64 s4
+    block, or the whole row for per-token scales) hold their maximum m in
+    element 0 and otherwise values at or within 3 ulp of a half-integer
+    multiple of s = fl(m / limit): the values where multiplying by a
+    reciprocal can round differently from the division. Group maxima run from
+    2^-140 (subnormal, and s below 2^-120) to 2^121."""
+    ng = K // group
+    e = rng.integers(-140, 121, (T, ng, 1)).astype(np.float64)
+    mx = (rng.uniform(1, 2, (T, ng, 1)) * np.exp2(e)).astype(np.float32)
+    s = mx / np.float32(limit)
+    h = rng.integers(-limit, limit, (T, ng, group)) + 0.5
+    v = (h * s.astype(np.float64)).astype(np.float32)
+    d = rng.integers(-3, 4, (T, ng, group))
+    for k in range(3):
+        v = np.where(d > k, np.nextafter(v, np.float32(np.inf)), v)
+        v = np.where(d < -k, np.nextafter(v, np.float32(-np.inf)), v)
+    v = np.clip(v, -mx, mx)
+    v[..., 0] = mx[..., 0] * np.where(rng.integers(0, 2, (T, ng)) == 1, 1, -1).astype(np.float32)
+    return v.reshape(T, K)
+
+
+@pytest.mark.parametrize("group,limit", [(32, 127), (4096, 127), (64, 7)])
+def test_rounding_boundary_rows_separate_division_from_reciprocal(group, limit):
+    # The GPU quantizers multiply by a reciprocal and divide only near a
+    # rounding boundary. Their tests use these rows, which must hold values
+    # where the two round differently, or a quantizer that skipped the
+    # division would pass them.
+    rng = np.random.default_rng(group + limit)
+    x = rounding_boundary_rows(rng, 2, 4096, group, limit)
+    if limit == 7:
+        q, s, _ = O.quantize_act_s4(x)
+    else:
+        q, s, _ = O.quantize_act(x, 32 if group == 32 else 0)
+    sb = np.repeat(s.reshape(2, -1), group, axis=1)
+    with np.errstate(all="ignore"):
+        div = np.clip(np.rint(x / sb), -limit, limit)
+        mul = np.clip(np.rint(x * (np.float32(1) / sb)), -limit, limit)
+    assert np.array_equal(div, q)                        # the oracle divides
+    assert np.count_nonzero(mul != q) > 0
+
+
 def test_silu_mul_and_rmsnorm_close_to_float64():
     rng = np.random.default_rng(5)
     g = (rng.standard_normal(4096) * 4).astype(np.float32)
