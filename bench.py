@@ -75,6 +75,14 @@ def launcher(cfg, act, outs):
 
 
 WARM_MS = 20.0      # warm-up GPU time before a timed region (the shader clock's ramp)
+# Cycles of torch's spin kernel enqueued after the pre-timing synchronize and
+# before a timed region's start event (nvbench's blocking-kernel method): it
+# holds the stream (~85 us) while the host submits the timed graph, so the
+# start event is stamped with the graph's launches already queued. Without it
+# the host's submission time sometimes lands inside the timed region: the
+# headline at 20 timed launches read 18.9-20.8 us without, 18.8-18.9 with
+# (1000 launches: 18.3). A longer spin (420 us) gave 18.7-19.3.
+SPIN_CYCLES = 200000
 
 
 def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
@@ -135,6 +143,8 @@ def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    if SPIN_CYCLES:
+        torch.cuda._sleep(SPIN_CYCLES)
     e0.record()
     gt.replay()
     e1.record()
@@ -739,8 +749,9 @@ def main():
     # Before its `warmup` launches the headline kernel also runs ~WARM_MS of
     # untimed launches, as every other line does: after the driver's 5
     # warm-up launches alone its 20 timed launches read 19.5-19.9 us, with
-    # the settle pass 19.2-19.4 us; 1000 timed launches read ~18.5 us (a
-    # replay carries a fixed ~14 us that 20 launches share).
+    # the settle pass 19.2-19.4 us, with the spin before the start event as
+    # well 18.8-18.9 us; 1000 timed launches read ~18.3 us (a replay still
+    # carries a fixed ~10 us on the device that 20 launches share).
     r = measure(head, args.steps, args.warmup, args.eager, settle_ms=WARM_MS)
     log(f"cfg1: {r['kernel_us']:.2f} us/launch, {r['GBps']:.1f} GB/s, exact={r['bit_exact_vs_oracle_rows0_512']}")
     if args.copy_mib:
@@ -757,6 +768,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_launches": r.get("settle_launches"),
+        "timing": "HIP events around one graph replay of the timed launches, after a "
+                  "synchronize and a ~85 us spin kernel that holds the stream while the "
+                  "replay is submitted",
         "ms_per_step": round(per * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
