@@ -65,35 +65,61 @@ def make_copies(ws, min_bytes=2 * MALL_BYTES + (64 << 20)):
     return copies, per * n
 
 
-def launcher(cfg, act, outs):
-    import torch
-    from knivesysl_xe_amd import ops
-    dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
-    if cfg.kind == "gemv":
-        return lambda w: ops.gemv(w[0], act, dt, out=outs[0])
-    return lambda w: ops.gemm_fanout(w, act, dt, offsets=cfg.offsets, outs=outs)
+class launcher:
+    """run(copy): one launch of the projection on weight copy `copy`. The
+    argument checks and marshalling of each copy are done once, by prepare()
+    or on the copy's first call (ops.PreparedGemv / PreparedGemmFanout), so a
+    call is one C-ABI call."""
+
+    def __init__(self, cfg, act, outs):
+        import torch
+        self.cfg, self.act, self.outs = cfg, act, outs
+        self.dt = torch.bfloat16 if cfg.out_bf16 else torch.float32
+        self.calls = {}
+
+    def prepare(self, copies):
+        from knivesysl_xe_amd import ops
+        for w in copies:
+            if id(w) not in self.calls:
+                self.calls[id(w)] = (
+                    ops.PreparedGemv(w[0], self.act, self.dt, out=self.outs[0]) if self.cfg.kind == "gemv"
+                    else ops.PreparedGemmFanout(w, self.act, self.dt, offsets=self.cfg.offsets, outs=self.outs))
+
+    def __call__(self, w):
+        if id(w) not in self.calls:
+            self.prepare([w])
+        self.calls[id(w)]()
 
 
 WARM_MS = 20.0      # warm-up GPU time before a timed region (the shader clock's ramp)
-# Cycles of torch's spin kernel enqueued after the pre-timing synchronize and
-# before a timed region's start event (nvbench's blocking-kernel method): it
-# holds the stream (~85 us) while the host submits the timed graph, so the
-# start event is stamped with the graph's launches already queued. Without it
-# the host's submission time sometimes lands inside the timed region: the
-# headline at 20 timed launches read 18.9-20.8 us without, 18.8-18.9 with
-# (1000 launches: 18.3). A longer spin (420 us) gave 18.7-19.3.
-SPIN_CYCLES = 200000
+# The timed region starts behind a hold kernel (ops.probe_hold, nvbench's
+# blocking kernel), enqueued after the pre-timing synchronize: one wave
+# polls a host-pinned flag that the host sets once it has submitted the
+# timed launches, so the start event is stamped with all of them queued and
+# the host's submission time stays out of the timed region (without a hold
+# the headline's 20 timed launches read 18.9-20.8 us, 18.3 us at 1000). A
+# graph replay also carries ~10 us of its own on the device, which 20
+# launches share and 1000 do not, so up to EAGER_TIMED_MAX timed launches
+# are issued one by one behind the hold, more as one graph replay. The hold
+# times out after HOLD_MAX_US; the JSON line says whether the flag released
+# it.
+HOLD_MAX_US = 20000
+EAGER_TIMED_MAX = 32
 
 
 def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
-    """Capture `steps` launches in one graph, replay it between syncs. With
-    warmup=None the warm-up graph holds about WARM_MS of launches, sized from
-    a replay of 10 (the clock ramps up over the first milliseconds of load, so
-    a fixed small count under-warms short kernels). settle_ms > 0 runs about
-    that much GPU time of untimed launches of the same kernel right before the
-    `warmup` launches (their count goes to info["settle_launches"]), so that
-    a short explicit warm-up does not start the timed launches on a clock
-    that is still ramping."""
+    """Time `steps` launches between HIP events after a synchronize: one
+    graph replay, or up to EAGER_TIMED_MAX launches issued one by one, in
+    both cases behind the hold kernel. The `warmup` launches run as one graph
+    replay before the synchronize. With warmup=None the warm-up graph holds
+    about WARM_MS of launches, sized from a replay of 10 (the clock ramps up
+    over the first milliseconds of load, so a fixed small count under-warms
+    short kernels). settle_ms > 0 runs about that much GPU time of untimed
+    launches of the same kernel right before the `warmup` launches (their
+    count goes to info["settle_launches"]), so that a short explicit warm-up
+    does not start the timed launches on a clock that is still ramping.
+    info["hold_released"] says whether the host's flag, not the time-out,
+    ended the hold before the timed launches."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -122,8 +148,9 @@ def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
         per_ms = max(e0.elapsed_time(e1) / 10, 1e-3)
         warmup = int(min(max(WARM_MS / per_ms, 20), 20000))
         del g10
+    eager = steps <= EAGER_TIMED_MAX
     gw = capture(max(warmup, 1), 0)
-    gt = capture(steps, max(warmup, 1))
+    gt = None if eager else capture(steps, max(warmup, 1))
     torch.cuda.synchronize()
     if settle_ms > 0:
         g10 = capture(10, 0)
@@ -141,15 +168,29 @@ def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
             info["settle_launches"] = 10 * (reps + 2)
     gw.replay()
     torch.cuda.synchronize()
+    from knivesysl_xe_amd import ops
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    if SPIN_CYCLES:
-        torch.cuda._sleep(SPIN_CYCLES)
+    ops.probe_hold(flag, HOLD_MAX_US, status)
     e0.record()
-    gt.replay()
-    e1.record()
+    try:
+        if eager:
+            for i in range(steps):
+                run(copies[(max(warmup, 1) + i) % len(copies)])
+        else:
+            gt.replay()
+        e1.record()
+    finally:
+        flag.fill_(1)                                   # release the hold
+    submit = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if info is not None:
+        info["submit_us"] = submit * 1e6
+        info["hold_released"] = int(status.item()) == 1
     return e0.elapsed_time(e1) / 1e3, wall
 
 
@@ -200,6 +241,7 @@ def measure(cfg, steps, warmup, eager=False, settle_ms=0.0):
     outs = [torch.empty(cfg.tokens, w.M, dtype=dt, device="cuda") for w in ws]
     run = launcher(cfg, act, outs)
     copies, rot_bytes = make_copies(ws)
+    run.prepare(copies)
     info = {}
     if eager:
         secs, wall = time_eager(run, copies, steps, warmup)
@@ -228,8 +270,9 @@ def measure(cfg, steps, warmup, eager=False, settle_ms=0.0):
         "quantize_us": quant_us,
         "wall_s": wall,
     }
-    if "settle_launches" in info:
-        res["settle_launches"] = info["settle_launches"]
+    for k in ("settle_launches", "hold_released", "submit_us"):
+        if k in info:
+            res[k] = info[k]
     res["roofline_frac"] = (res["GBps"] / HBM_PEAK_GBS if cfg.bound == "hbm"
                             else res["TOPS"] / INT8_PEAK_TOPS)
     del copies, ws, outs
@@ -749,9 +792,8 @@ def main():
     # Before its `warmup` launches the headline kernel also runs ~WARM_MS of
     # untimed launches, as every other line does: after the driver's 5
     # warm-up launches alone its 20 timed launches read 19.5-19.9 us, with
-    # the settle pass 19.2-19.4 us, with the spin before the start event as
-    # well 18.8-18.9 us; 1000 timed launches read ~18.3 us (a replay still
-    # carries a fixed ~10 us on the device that 20 launches share).
+    # the settle pass 19.2-19.4 us; issued one by one behind the hold kernel
+    # they read as the 1000-launch replay does (~18.3-18.5 us).
     r = measure(head, args.steps, args.warmup, args.eager, settle_ms=WARM_MS)
     log(f"cfg1: {r['kernel_us']:.2f} us/launch, {r['GBps']:.1f} GB/s, exact={r['bit_exact_vs_oracle_rows0_512']}")
     if args.copy_mib:
@@ -768,9 +810,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_launches": r.get("settle_launches"),
-        "timing": "HIP events around one graph replay of the timed launches, after a "
-                  "synchronize and a ~85 us spin kernel that holds the stream while the "
-                  "replay is submitted",
+        "timing": "HIP events around the timed launches (up to 32: issued one by one; more: "
+                  "one graph replay), after a synchronize and a kernel that holds the stream "
+                  "until the host has submitted them",
+        "hold_released": r.get("hold_released"),
         "ms_per_step": round(per * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",

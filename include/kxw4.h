@@ -339,6 +339,14 @@ int kxw4_probe_read_shapes(void);
  * -6. */
 int kxw4_probe_issue(int mode, int waves_per_simd, int iters, float *sink, int sink_words,
                      double *blocks, void *stream);
+/* kxw4_probe_hold: one wave that holds `stream` until the host sets *flag
+ * (host-pinned memory, e.g. hipHostMalloc) to nonzero or max_us (1 ..
+ * 1000000) microseconds have passed, then writes 1 (released) or 2 (timed
+ * out) to *status (device memory). A timing harness enqueues it before its
+ * start event and sets the flag after submitting the timed launches, so the
+ * host's submission time stays out of the timed region (nvbench's blocking
+ * kernel). No counterpart in the reference. Returns 0, -1 or -6. */
+int kxw4_probe_hold(const uint32_t *flag, int max_us, uint32_t *status, void *stream);
 
 /* Debug: exact int32 unit partials P[T][M][K/unit] (unit = 32 for block 32,
  * else group), from the same unpack and MFMA code as the projections. */

@@ -73,6 +73,7 @@ SIGNATURES = {
     "kxw4_probe_read": (I, [P, C.c_size_t, I, P, I, P]),
     "kxw4_probe_read_shapes": (I, []),
     "kxw4_probe_issue": (I, [I, I, I, P, I, C.POINTER(C.c_double), P]),
+    "kxw4_probe_hold": (I, [P, I, P, P]),
     "kxw4_partials": (I, [WP, AP, P, P]),
 }
 

@@ -172,6 +172,27 @@ constexpr ReadShape kReadShapes[] = {
 };
 constexpr int kReadShapeCount = sizeof(kReadShapes) / sizeof(kReadShapes[0]);
 
+// A wave that holds its stream until the host sets *flag (host-pinned
+// memory, read at system scope) or max_ticks of the constant-rate wall clock
+// have passed, whichever comes first, then writes 1 (released by the flag)
+// or 2 (timed out) to *status. A timing harness enqueues it before its start
+// event and sets the flag once it has submitted the timed launches, so the
+// start event is stamped with all of them queued (nvbench's blocking
+// kernel). Every lane polls the same word; lane 0 writes the status.
+__global__ __launch_bounds__(64) void probe_hold_kernel(const uint32_t *flag, long long max_ticks,
+                                                        uint32_t *status) {
+    const long long t0 = wall_clock64();
+    uint32_t st = 1;
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0) {
+        if (wall_clock64() - t0 > max_ticks) {
+            st = 2;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+    if (threadIdx.x == 0) *status = st;
+}
+
 }  // namespace kxw4
 
 using namespace kxw4;
@@ -234,4 +255,17 @@ extern "C" int kxw4_probe_issue(int mode, int waves_per_simd, int iters, float *
     // blocks per SIMD: 4 per iteration and wave (split roles: per role pair)
     if (blocks) *blocks = 4.0 * iters * (mode == 3 ? waves_per_simd / 2 : waves_per_simd);
     return groups * 4 * waves_per_simd;
+}
+
+extern "C" int kxw4_probe_hold(const uint32_t *flag, int max_us, uint32_t *status, void *stream) {
+    using namespace kxw4;
+    if (!flag || !status || max_us <= 0 || max_us > 1000000) return KXW4_EARG;
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+        return KXW4_EHIP;
+    const long long ticks = (long long)max_us * khz / 1000;
+    hipLaunchKernelGGL(probe_hold_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), flag, ticks,
+                       status);
+    return hipGetLastError() == hipSuccess ? 0 : KXW4_EHIP;
 }

@@ -410,6 +410,53 @@ def gemm_fanout(ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offset
     return ys
 
 
+class PreparedGemv:
+    """gemv with its checks and argument marshalling done once: each call is
+    one kxw4_gemv on the current stream, for loops that launch the same
+    projection on the same buffers (serving steps, benchmarks). The tensors
+    must stay alive and keep their shapes; their contents may change."""
+
+    def __init__(self, w: W4Weight, a: QuantAct, dtype=torch.float32, residual=None,
+                 splits: int = 0, out=None):
+        dev = w.codes.device
+        _check_weight(w, dev)
+        _check_act(a, dev)
+        self.y = _out(a.T, w.M, dtype, dev, out)
+        _residual(residual, a.T, w.M, dev)
+        self._keep = (w, a, residual)
+        self._wc, self._ac = w.c(), a.c()
+        self._args = (C.byref(self._wc), C.byref(self._ac), _ptr(self.y), _dtype_code(dtype),
+                      _ptr(residual), splits)
+
+    def __call__(self) -> torch.Tensor:
+        check("kxw4_gemv", lib().kxw4_gemv(*self._args, _stream()))
+        return self.y
+
+
+class PreparedGemmFanout:
+    """gemm_fanout with its checks and argument marshalling done once: each
+    call is one kxw4_gemm_fanout on the current stream (see PreparedGemv)."""
+
+    def __init__(self, ws: Sequence[W4Weight], a: QuantAct, dtype=torch.float32, offsets=None,
+                 forced_splits: int = 0, outs=None):
+        dev = ws[0].codes.device
+        for w in ws:
+            _check_weight(w, dev)
+        _check_act(a, dev)
+        self.ys = _outs(ws, a.T, dtype, dev, outs)
+        self._keep = (list(ws), a)
+        self._wcs, self._warr = _weight_array(ws)
+        self._yarr = (C.c_void_p * len(ws))(*[y.data_ptr() for y in self.ys])
+        self._off, nseg = _offsets(offsets)
+        self._ac = a.c()
+        self._args = (self._warr, self._yarr, len(ws), C.byref(self._ac), _dtype_code(dtype),
+                      self._off, nseg, forced_splits)
+
+    def __call__(self):
+        check("kxw4_gemm_fanout", lib().kxw4_gemm_fanout(*self._args, _stream()))
+        return self.ys
+
+
 def gemm_w4a4(w: W4Weight, a: QuantActS4, dtype=torch.float32, residual=None,
               out=None) -> torch.Tensor:
     """W4A4 GEMM of s4 activations against a K64 weight with FP16|zp scales."""
@@ -536,6 +583,18 @@ def probe_mfma_i8(shape: int, iters: int, sink: torch.Tensor) -> tuple:
     if n < 0:
         raise _lib.KxError("kxw4_probe_mfma_i8", n)
     return n, ops_count.value
+
+
+def probe_hold(flag: torch.Tensor, max_us: int, status: torch.Tensor) -> None:
+    """Enqueue the stream hold on the current stream: it waits until the host
+    sets flag[0] (a pinned CPU int32 tensor) to nonzero or max_us pass, then
+    writes 1 (released) or 2 (timed out) to status[0] (a device int32
+    tensor)."""
+    if (flag.device.type != "cpu" or not flag.is_pinned() or flag.dtype != torch.int32
+            or status.device.type != "cuda" or status.dtype != torch.int32):
+        raise _lib.KxError("kxw4_probe_hold", _lib.EARG)
+    check("kxw4_probe_hold", lib().kxw4_probe_hold(C.c_void_p(flag.data_ptr()), int(max_us), _ptr(status),
+                                                   _stream()))
 
 
 def probe_issue(mode: int, waves_per_simd: int, iters: int, sink: torch.Tensor) -> tuple:

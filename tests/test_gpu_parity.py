@@ -725,6 +725,34 @@ def test_gemv_fanout(rows, T, block, enc, group):
         assert_parity(to_np(y), ref, f"fanout rows={c.shape[0]}")
 
 
+def test_prepared_calls_match_the_checked_calls():
+    # ops.PreparedGemv / PreparedGemmFanout marshal once and then make the
+    # same C-ABI call: the oracle's bits on every call, also after the
+    # activation buffer's contents change
+    rng = np.random.default_rng(21)
+    K, rows, T = 2048, [1024, 512], 8
+    wts = [rand_weight(rng, M, K, 128, 0) for M in rows]
+    ws = [weight(c, sc, 128, 0) for c, sc in wts]
+    x1 = rng.standard_normal((T, K)).astype(np.float32)
+    x2 = rng.standard_normal((T, K)).astype(np.float32)
+    a = ops.quantize_act(dev(x1), 0)
+    outs = [torch.empty(T, M, dtype=torch.bfloat16, device=DEV) for M in rows]
+    fan = ops.PreparedGemmFanout(ws, a, torch.bfloat16, outs=outs)
+    one = ops.PreparedGemv(ws[0], a, torch.float32)
+    for x in (x1, x2, x1):
+        ops.quantize_act(dev(x), 0, out=a)
+        q, s, sm = O.quantize_act(x, 0)
+        fan()
+        y = one()
+        for (c, sc), got in zip(wts, outs):
+            sp = O.segment_splits(T, c.shape[0], K, None, 0)
+            ref = O.project(c, sc, 128, 0, q, s, sm, 0, O.VAR_GEMM, sp, out_bf16=True)
+            assert_parity(to_np(got), ref, "prepared fan-out", bf16=True)
+        ref = O.project(wts[0][0], wts[0][1], 128, 0, q, s, sm, 0, O.VAR_GEMV,
+                        O.gemv_splits(rows[0] // 16))
+        assert_parity(to_np(y), ref, "prepared gemv")
+
+
 @pytest.mark.parametrize("M,K,T,block,enc,group,forced", [
     (17408 // 4, 5120, 8, 32, 1, 32, 0), (5120, 5120, 24, 32, 1, 64, 0), (1024, 2048, 128, 32, 1, 32, 0),
     (5120, 5120, 8, 0, 0, 128, 16), (768, 4096, 200, 0, 0, 64, 0), (512, 2048, 40, 0, 0, 128, 0),

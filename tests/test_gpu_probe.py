@@ -2,7 +2,9 @@
 xpu/probe/dpas_probe.cpp): the all-ones MFMA chains must end at exactly
 iters * K in every wave (the reference's `d == iters * K` check), the read
 probe must cover the buffer, the issue probe must write one deterministic word
-per wave, and all of them must reject bad arguments.
+per wave, and all of them must reject bad arguments. The timing harness's
+stream hold (kxw4_probe_hold) must end on the host's flag, or on its own
+bound when the flag stays clear.
 """
 import pytest
 
@@ -95,3 +97,44 @@ def test_issue_probe_arguments():
         ops.probe_issue(0, 1, 1, sink[:16])          # sink too small
     with pytest.raises(KxError):
         ops.probe_issue(0, 1, 1, sink.view(torch.int32))  # float32 sink only
+
+
+def test_hold_released_by_the_host_flag():
+    # the hold keeps the stream until the host sets the pinned flag: work
+    # queued behind it waits, then runs; status 1 = released by the flag
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.zeros(1, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ops.probe_hold(flag, 200000, status)
+    out.add_(1.0)                                   # queued behind the hold
+    e = torch.cuda.Event()
+    e.record()
+    assert not e.query()                            # still held: the flag is not set
+    flag.fill_(1)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1 and float(out.item()) == 1.0
+
+
+def test_hold_times_out_when_the_flag_stays_clear():
+    # the host never sets the flag: the hold's own bound ends it (status 2)
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    ops.probe_hold(flag, 3000, status)
+    e1.record()
+    torch.cuda.synchronize()
+    assert int(status.item()) == 2
+    assert 2.5 <= e0.elapsed_time(e1) <= 50.0       # ms: about the 3 ms bound
+
+
+def test_hold_arguments():
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pinned = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    for flag, max_us in ((torch.zeros(1, dtype=torch.int32), 1000),        # not pinned
+                         (pinned, 0), (pinned, 2000000),
+                         (torch.zeros(1, dtype=torch.int32, device="cuda"), 1000)):
+        with pytest.raises(KxError):
+            ops.probe_hold(flag, max_us, status)
