@@ -92,25 +92,28 @@ class launcher:
 
 
 WARM_MS = 20.0      # warm-up GPU time before a timed region (the shader clock's ramp)
-# The timed region starts behind a hold kernel (ops.probe_hold, nvbench's
-# blocking kernel), enqueued after the pre-timing synchronize: one wave
-# polls a host-pinned flag that the host sets once it has submitted the
-# timed launches, so the start event is stamped with all of them queued and
-# the host's submission time stays out of the timed region (without a hold
-# the headline's 20 timed launches read 18.9-20.8 us, 18.3 us at 1000). A
-# graph replay also carries ~10 us of its own on the device, which 20
-# launches share and 1000 do not, so up to EAGER_TIMED_MAX timed launches
-# are issued one by one behind the hold, more as one graph replay. The hold
-# times out after HOLD_MAX_US; the JSON line says whether the flag released
-# it.
+# Timed regions of up to EAGER_TIMED_MAX launches (the driver's
+# `--steps 20`) are issued one by one behind a hold kernel (ops.probe_hold,
+# nvbench's blocking kernel), enqueued after the pre-timing synchronize: one
+# wave polls a host-pinned flag that the host sets once it has submitted the
+# timed launches, so the start event is stamped with all of them queued.
+# Without it the host's submission sometimes lands inside the timed region
+# (the headline's 20 launches in one graph replay read 18.9-20.8 us, behind
+# the hold 18.4-18.5 us), and a graph replay carries ~10 us of its own on
+# the device, which 20 launches share. Longer regions replay one graph right
+# after the synchronize: their submission is a small part of the region,
+# while a hold idles the GPU for the whole submission (under rocprofv3 ~10
+# ms per replay, which lowered the clock the GEMM lines then started on).
+# The hold times out after HOLD_MAX_US; the JSON line says whether the flag
+# released it.
 HOLD_MAX_US = 20000
 EAGER_TIMED_MAX = 32
 
 
 def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
     """Time `steps` launches between HIP events after a synchronize: one
-    graph replay, or up to EAGER_TIMED_MAX launches issued one by one, in
-    both cases behind the hold kernel. The `warmup` launches run as one graph
+    graph replay, or up to EAGER_TIMED_MAX launches issued one by one behind
+    the hold kernel. The `warmup` launches run as one graph
     replay before the synchronize. With warmup=None the warm-up graph holds
     about WARM_MS of launches, sized from a replay of 10 (the clock ramps up
     over the first milliseconds of load, so a fixed small count under-warms
@@ -174,7 +177,8 @@ def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ops.probe_hold(flag, HOLD_MAX_US, status)
+    if eager:
+        ops.probe_hold(flag, HOLD_MAX_US, status)
     e0.record()
     try:
         if eager:
@@ -190,7 +194,8 @@ def time_graph(run, copies, steps, warmup, settle_ms=0.0, info=None):
     wall = time.perf_counter() - t0
     if info is not None:
         info["submit_us"] = submit * 1e6
-        info["hold_released"] = int(status.item()) == 1
+        if eager:
+            info["hold_released"] = int(status.item()) == 1
     return e0.elapsed_time(e1) / 1e3, wall
 
 
@@ -810,9 +815,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_launches": r.get("settle_launches"),
-        "timing": "HIP events around the timed launches (up to 32: issued one by one; more: "
-                  "one graph replay), after a synchronize and a kernel that holds the stream "
-                  "until the host has submitted them",
+        "timing": "HIP events around the timed launches after a synchronize: up to 32 issued "
+                  "one by one behind a kernel that holds the stream until the host has submitted "
+                  "them; more as one graph replay",
         "hold_released": r.get("hold_released"),
         "ms_per_step": round(per * 1e3, 6),
         "higher_is_better": True,
