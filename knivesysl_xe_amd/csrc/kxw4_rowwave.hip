@@ -328,6 +328,9 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // repeat rows 0-7 and are never stored) and its K-slot group
     const int ta = TT <= 8 ? min(n & 7, T - 1) : min(n, T - 1);
     const int8_t *abase = Act + (size_t)ta * pitch + 16 * g4;
+    // K16 with one or two tokens: whether this lane's activation bytes (K
+    // slots 8*g4 .. 8*g4+7 of each unit, row n) belong to its row's half
+    const bool k16_keep = (n < 8) == (g4 < 2);
     float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
     if (active) {
@@ -357,8 +360,17 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                 for (int p = 0; p < PF; ++p) {
                     const int i = ib + p;
                     const int kb = kt0 + i;
-                    const v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
-                    const v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
+                    v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
+                    v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
+                    if constexpr (K16 && NR < 4) {
+                        // K16 with one or two tokens: MFMA row t + 8h carries
+                        // half h of token t (rows 0-7 keep K slots 0-15, lane
+                        // groups 0-1; rows 8-15 slots 16-31, lane groups
+                        // 2-3), so one MFMA per unit gives both half partials
+                        const v4i z4 = {0, 0, 0, 0};
+                        A0 = k16_keep ? A0 : z4;
+                        A1 = k16_keep ? A1 : z4;
+                    }
                     const v4u wd = ring[p][0];
                     // W8: unit j's scale of this lane's row, from lane n + 16j
                     uint32_t s8[W8 ? 4 : 1];
@@ -439,12 +451,22 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
                                     const uint32_t lo = ((((d ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
                                     const uint32_t hi = (((((d >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
                                     bv = (long)((uint64_t)lo | ((uint64_t)hi << 32));
-                                    const v4i ph[2] = {mfma_k32(av, g4 < 2 ? bv : 0l, zero), mfma_k32(av, g4 < 2 ? 0l : bv, zero)};
+                                    // half 0 of token r in register r of lanes 0-15,
+                                    // half 1 in lanes 32-47, brought down 32 lanes (the
+                                    // swap's other operand, whose low lanes it
+                                    // overwrites, is a register no token uses: r + 2)
+                                    const v4i acc1 = mfma_k32(av, bv, zero);
+                                    int ph1[NR];
+#pragma unroll
+                                    for (int r = 0; r < NR; ++r)
+                                        ph1[r] = (int)__builtin_amdgcn_permlane32_swap((unsigned)acc1[r], (unsigned)acc1[r + 2],
+                                                                                      false, false)[1];
 #pragma unroll
                                     for (int h = 0; h < 2; ++h) {
                                         const float ws = half_bits_to_float((uint16_t)((h ? s1 : s0) & 0xFFF0u));
 #pragma unroll
-                                        for (int r = 0; r < NR; ++r) f0[r] = __builtin_fmaf((float)ph[h][r] * ws, zas[j][r], f0[r]);
+                                        for (int r = 0; r < NR; ++r)
+                                            f0[r] = __builtin_fmaf((float)(h ? ph1[r] : acc1[r]) * ws, zas[j][r], f0[r]);
                                     }
                                     // (with one or two tokens the registers allow a
                                     // tile's units to overlap; the chain updates stay
