@@ -61,6 +61,11 @@ namespace kxw4 {
 constexpr size_t kRwLdsMax = 160 * 1024;
 constexpr int kRwSplitWaves = 8;            // most waves that share one slice's splits
 constexpr int kRwMaxHalves = 2;             // halves of a slice: one 16-row window
+// zero words at the end of the work-group's LDS: 16 (a padded position's
+// scale reads), 144 for the one- and two-token K16 instances (a 4-tile
+// ring's activation reads of the lanes that hold the other half: 4*128 + 64
+// bytes)
+constexpr int kRwK16ZeroWords = 144;
 
 enum { kWfW4 = 0, kWfW8 = 1, kWfK16 = 2 };     // weight format of a row-wave instance
 
@@ -109,6 +114,8 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
     // undoes the nibble unpack's factor 16 (the folded and W8/K16 bytes have none)
     constexpr float kInv16 = WF != kWfW4 || ZF ? 1.0f : 0.0625f;
     static_assert(PF % 2 == 0, "the GEMV accumulator parity assumes an even ring");
+    static_assert(!(K16 && NR < 4) || PF * kTileK + 64 <= 4 * kRwK16ZeroWords,
+                  "a ring's zero reads stay inside the zero words");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     const int nthreads = blockDim.x, tid = threadIdx.x;
@@ -319,7 +326,10 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             }
         }
     }
-    if (tid < 16) Zero[tid] = 0.0f;
+    // (K16 with one or two tokens: 144 words, which the lanes whose
+    // activation bytes belong to the other half read for a ring's tiles)
+    // (a work-group may have fewer threads than words)
+    for (int i = tid; i < (K16 && NR < 4 ? kRwK16ZeroWords : 16); i += nthreads) Zero[i] = 0.0f;
     lds_sync_after_dma();
 
     // ---- streaming: one chain per split, in registers ----
@@ -355,22 +365,21 @@ __global__ __launch_bounds__(64 * rw_max_waves(WF, PF)) void rowwave_kernel(cons
             auto ring_pass = [&](int ib, auto pred, auto loads) {
                 constexpr bool PRED = decltype(pred)::value;
                 constexpr bool LOADS = decltype(loads)::value;
-                const int8_t *ar = abase + (size_t)(kt0 + ib) * kTileK;
+                // K16 with one or two tokens: lanes holding the other half's
+                // K slots read zeros (the ring's tiles are immediate offsets
+                // 0 .. PF*128+64 from the zero area)
+                const int8_t *ar = K16 && NR < 4 && !k16_keep ? reinterpret_cast<const int8_t *>(Zero)
+                                                             : abase + (size_t)(kt0 + ib) * kTileK;
 #pragma unroll
                 for (int p = 0; p < PF; ++p) {
                     const int i = ib + p;
                     const int kb = kt0 + i;
-                    v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
-                    v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
-                    if constexpr (K16 && NR < 4) {
-                        // K16 with one or two tokens: MFMA row t + 8h carries
-                        // half h of token t (rows 0-7 keep K slots 0-15, lane
-                        // groups 0-1; rows 8-15 slots 16-31, lane groups
-                        // 2-3), so one MFMA per unit gives both half partials
-                        const v4i z4 = {0, 0, 0, 0};
-                        A0 = k16_keep ? A0 : z4;
-                        A1 = k16_keep ? A1 : z4;
-                    }
+                    // (K16 with one or two tokens: MFMA row t + 8h carries half
+                    // h of token t -- rows 0-7 keep K slots 0-15, lane groups
+                    // 0-1, rows 8-15 slots 16-31, lane groups 2-3 -- so one
+                    // MFMA per unit gives both half partials)
+                    const v4i A0 = *reinterpret_cast<const v4i *>(ar + p * kTileK);
+                    const v4i A1 = *reinterpret_cast<const v4i *>(ar + p * kTileK + 64);
                     const v4u wd = ring[p][0];
                     // W8: unit j's scale of this lane's row, from lane n + 16j
                     uint32_t s8[W8 ? 4 : 1];
@@ -805,7 +814,7 @@ int launch_rowwave(DecodeArgs &a, hipStream_t st) {
     auto lds_for = [&](int T) {
         return (size_t)T * (a.K + 16) + (wf == kWfW8 || (wf == kWfW4 && mode == 0 && unit == 64) ? 0 : (size_t)grmax * g * 32) +
                (mode != 0 ? (size_t)(zp_table ? 2 : 1) * nu * 16 * 4 : 0) +
-               (S > 1 ? (size_t)spw * (S - 1) * 256 * 4 : 0) + 64;
+               (S > 1 ? (size_t)spw * (S - 1) * 256 * 4 : 0) + (wf == kWfK16 && T <= 2 ? 4 * kRwK16ZeroWords : 64);
     };
     size_t lds = lds_for(a.T);
     if (lds > kRwLdsMax) {
