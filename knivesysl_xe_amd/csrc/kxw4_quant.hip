@@ -52,6 +52,43 @@ __device__ __forceinline__ int half_wave_sum(int v) {
     return v;
 }
 
+// Lane reductions on DPP moves (no LDS round trip per step), for max and
+// integer sums, whose result does not depend on the order: quad_perm
+// [1,0,3,2] and [2,3,0,1] exchange the neighbours and pairs of a 4-lane
+// group, row_half_mirror (lane i <-> 7-i of each 8) joins two groups,
+// row_mirror (i <-> 15-i of each 16) two halves of a row, and lanes 0, 16,
+// 32 and 48 then hold the four rows' results. Every lane of the group being
+// reduced must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    return fmaxf(v, dpp_f<kDppQuadXor2>(v));
+}
+__device__ __forceinline__ int quad_sum(int v) {
+    v += dpp_i<kDppQuadXor1>(v);
+    return v + dpp_i<kDppQuadXor2>(v);
+}
+__device__ __forceinline__ float oct_max(float v) {
+    v = quad_max(v);
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+__device__ __forceinline__ int oct_sum(int v) {
+    v = quad_sum(v);
+    return v + dpp_i<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = oct_max(v);
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    const int b = __float_as_int(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)), __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
+}
+
 __device__ __forceinline__ float block_reduce_max(float v, float *red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -315,8 +352,7 @@ __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
             }
         }
         // work-group max (order-free, so any thread count gives the same bits)
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        mx = wave_max(mx);
         if ((tid & 63) == 0) red[tid >> 6] = mx;
         __syncthreads();
         mx = red[0];
@@ -337,15 +373,13 @@ __global__ __launch_bounds__(NT) void quantize_tok_kernel(QuantArgs a) {
                 float mx = fabsf(v[c][0]);
 #pragma unroll
                 for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
-                mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+                mx = quad_max(mx);
                 s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
             }
             int sum = 0;
             const uint2 codes = quantize_chunk(v[c], s, sum);
             if (in) *reinterpret_cast<uint2 *>(qrow + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) = codes;
-            sum += __shfl_xor(sum, 1, 64);
-            sum += __shfl_xor(sum, 2, 64);
+            sum = quad_sum(sum);
             if (in && (idx & 3) == 0) {
                 if (!PER_TOKEN) a.scale[(size_t)t * (K / 32) + (idx >> 2)] = s;
                 if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
@@ -388,8 +422,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_spread_kernel(QuantArgs a,
                 for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
             }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        mx = wave_max(mx);
         if ((tid & 63) == 0) red[tid >> 6] = mx;
         __syncthreads();
         mx = red[0];
@@ -412,8 +445,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_spread_kernel(QuantArgs a,
         float mx = fabsf(w[0]);
 #pragma unroll
         for (int j = 1; j < 8; ++j) mx = fmaxf(mx, fabsf(w[j]));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        mx = quad_max(mx);
         s = (mx > 0.0f) ? (mx / 127.0f) : 1.0f;
     }
     if (P >= kSiluMul && a.out && in) store_chunk_out<1>(a, t, idx, w);
@@ -422,8 +454,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_spread_kernel(QuantArgs a,
     if (in)
         *reinterpret_cast<uint2 *>(a.q + (size_t)t * K + 64 * (idx >> 3) + 16 * (idx & 3) + 8 * ((idx >> 2) & 1)) =
             codes;
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    sum = quad_sum(sum);
     if (in && (idx & 3) == 0) {
         if (!PER_TOKEN) a.scale[(size_t)t * (K / 32) + (idx >> 2)] = s;
         if (a.sum) a.sum[(size_t)t * (K / 32) + (idx >> 2)] = sum;
@@ -538,9 +569,7 @@ __global__ __launch_bounds__(256) void quantize_s4_kernel(const void *x, int T, 
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    mx = oct_max(mx);
     const float s = (mx > 0.0f) ? (mx / 7.0f) : 1.0f;
     float k[8];
     rint_quot(v, s, k);
@@ -552,9 +581,7 @@ __global__ __launch_bounds__(256) void quantize_s4_kernel(const void *x, int T, 
         sm += q;
         w |= (uint32_t)(q & 0xF) << (j < 4 ? 8 * j : 8 * (j - 4) + 4);
     }
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
-    sm += __shfl_xor(sm, 4, 64);
+    sm = oct_sum(sm);
     if (live) {
         const int kb = idx >> 4, c = idx & 15;
         q4[((size_t)kb * T + t) * 16 + 4 * (c & 3) + (c >> 2)] = w;
